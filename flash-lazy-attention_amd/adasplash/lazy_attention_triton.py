@@ -1,0 +1,109 @@
+"""Lazy attention (elastic softmax with a windowed head-wise bias) on the gfx950 HIP kernels.
+
+Drop-in for ``lazy_attention_triton(q, k, v, bias, tau, window_size=None, varlen=None)``
+and ``LazyAttentionTritonFunc`` (reference lazy_attention_triton.py:503-541):
+
+    out_i = sum_{j <= i} relu(softmax_j(q_i.k_j/sqrt(D) + bias[h, i-j]*1[0 <= i-j < W]) + tau_h/(i+1)) v_j
+
+q, k, v: [B, H, L, D] (RoPE already applied), bias [H, >= W], tau [H], varlen optional [B].
+Gradients: dq, dk, dv in the input dtype; dbias / dtau in float32 and only when bias / tau
+require grad (lazy_attention_triton.py:523-539).  Rows i >= varlen[b] are zero in the output
+and in every gradient.
+"""
+import torch
+
+from ._lib import (
+    DTYPE_CODE,
+    check,
+    check_inputs,
+    kernel_head_dim,
+    lib,
+    prep_bhld,
+    prep_varlen,
+    ptr,
+    stream_of,
+    t4,
+)
+
+
+def _params(bias, tau, H, window_size):
+    if bias.dim() != 2 or bias.shape[0] != H:
+        raise ValueError(f"bias must be [H={H}, W], got {tuple(bias.shape)}")
+    if tau.numel() != H:
+        raise ValueError(f"tau must have H={H} entries")
+    W = int(window_size)
+    if W <= 0 or W > bias.shape[1]:
+        raise ValueError(f"window_size={W} must lie in [1, bias.shape[1]={bias.shape[1]}]")
+    b32 = bias.detach().to(torch.float32).contiguous()
+    t32 = tau.detach().reshape(H).to(torch.float32).contiguous()
+    return b32, t32, W
+
+
+def _forward(q, k, v, bias, tau, window_size, varlen, need_w):
+    D, scale = check_inputs(q, k, v)
+    Dk = kernel_head_dim(D)
+    qp, kp, vp = (prep_bhld(x, Dk) for x in (q, k, v))
+    B, H, L, _ = qp.shape
+    b32, t32, W = _params(bias, tau, H, window_size)
+    vl = prep_varlen(varlen, B, q.device)
+    out = torch.empty((B, H, L, Dk), device=q.device, dtype=q.dtype)
+    lse = torch.empty((B, H, L), device=q.device, dtype=torch.float32)
+    wd = torch.empty((B, H, L, Dk), device=q.device, dtype=torch.float32) if need_w else None
+    rc = lib().fla_lazy_fwd(
+        t4(qp), t4(kp), t4(vp), t4(out), ptr(b32), b32.shape[1], ptr(t32), W, ptr(lse), ptr(wd), ptr(vl),
+        B, H, L, Dk, DTYPE_CODE[q.dtype], scale, stream_of(q),
+    )
+    check(rc, "fla_lazy_fwd")
+    return out, lse, wd, (qp, kp, vp), b32, t32, W, vl, D, Dk, scale
+
+
+class LazyAttentionTritonFunc(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, bias, tau, window_size, varlen=None):
+        out, lse, wd, (qp, kp, vp), b32, t32, W, vl, D, Dk, scale = _forward(
+            q, k, v, bias, tau, window_size, varlen, True
+        )
+        ctx.save_for_backward(qp, kp, vp, b32, t32, lse, wd, vl)
+        ctx.cfg = (W, D, Dk, scale, tuple(bias.shape))
+        ctx.tau_shape = tuple(tau.shape)
+        return out[..., :D] if Dk != D else out
+
+    @staticmethod
+    def backward(ctx, do):
+        qp, kp, vp, b32, t32, lse, wd, vl = ctx.saved_tensors
+        W, D, Dk, scale, bshape = ctx.cfg
+        B, H, L, _ = qp.shape
+        need = ctx.needs_input_grad[3] or ctx.needs_input_grad[4]
+        dop = prep_bhld(do.to(qp.dtype), Dk)
+        dq = torch.empty_like(qp)
+        dk = torch.empty_like(kp)
+        dv = torch.empty_like(vp)
+        dbias = torch.empty((H, W), device=qp.device, dtype=torch.float32) if need else None
+        dtau = torch.empty((H,), device=qp.device, dtype=torch.float32) if need else None
+        nbytes = int(lib().fla_lazy_bwd_workspace_size(B, H, L, W))
+        ws = torch.empty((nbytes,), device=qp.device, dtype=torch.uint8)
+        rc = lib().fla_lazy_bwd(
+            t4(qp), t4(kp), t4(vp), t4(dop), t4(dq), t4(dk), t4(dv), ptr(b32), b32.shape[1], ptr(t32), W,
+            ptr(lse), ptr(wd), ptr(vl), ptr(dbias), ptr(dtau), ptr(ws), nbytes, B, H, L, Dk,
+            DTYPE_CODE[qp.dtype], scale, stream_of(qp),
+        )
+        check(rc, "fla_lazy_bwd")
+        if Dk != D:
+            dq, dk, dv = dq[..., :D], dk[..., :D], dv[..., :D]
+        if need and bshape[1] != W:
+            full = torch.zeros(bshape, device=qp.device, dtype=torch.float32)
+            full[:, :W] = dbias
+            dbias = full
+        if need:
+            dtau = dtau.reshape(ctx.tau_shape)
+        return dq, dk, dv, dbias, dtau, None, None
+
+
+def lazy_attention_triton(q, k, v, bias, tau, window_size=None, varlen=None):
+    if window_size is None:
+        window_size = bias.shape[1]
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v, bias, tau)):
+        return LazyAttentionTritonFunc.apply(q, k, v, bias, tau, window_size, varlen)
+    out, *_rest = _forward(q, k, v, bias, tau, window_size, varlen, False)
+    D = q.shape[-1]
+    return out[..., :D] if out.shape[-1] != D else out

@@ -1,0 +1,222 @@
+// C ABI entry points (declared in include/flashlazy.h): argument validation and dispatch
+// on dtype / head dim / alpha.  Nothing here allocates; all launches are asynchronous on
+// the caller's stream.
+#include "args.h"
+#include "flashlazy_internal.h"
+
+using namespace fla;
+
+namespace {
+
+int elem_size(int dtype) { return dtype == FLA_F32 ? 4 : 2; }
+
+bool good_tensor(const fla_tensor4_t* t, int dtype) {
+  if (!t || !t->data) return false;
+  const int es = elem_size(dtype);
+  if (((uintptr_t)t->data) % 16) return false;
+  if ((t->stride_b * es) % 16 || (t->stride_h * es) % 16 || (t->stride_l * es) % 16) return false;
+  return true;
+}
+
+Tensor4 T4(const fla_tensor4_t* t) {
+  Tensor4 r;
+  r.data = t->data;
+  r.sb = t->stride_b;
+  r.sh = t->stride_h;
+  r.sl = t->stride_l;
+  return r;
+}
+
+bool good_common(int B, int H, int L, int D, int dtype) {
+  if (B <= 0 || H <= 0 || L <= 0 || L > (1 << 17)) return false;
+  if (D != 32 && D != 64 && D != 128) return false;
+  if (dtype != FLA_F32 && dtype != FLA_F16 && dtype != FLA_BF16) return false;
+  if ((int64_t)B * H * ((L + 127) / 128) > 0x7fffffffLL) return false;
+  return true;
+}
+
+
+}  // namespace
+
+#define FLA_DISPATCH(LAUNCH, ARGS, ...)                                           \
+  switch (dtype * 1000 + D) {                                                     \
+    case FLA_F32 * 1000 + 32: e = LAUNCH<F32, 32>(ARGS, ##__VA_ARGS__); break;    \
+    case FLA_F32 * 1000 + 64: e = LAUNCH<F32, 64>(ARGS, ##__VA_ARGS__); break;    \
+    case FLA_F32 * 1000 + 128: e = LAUNCH<F32, 128>(ARGS, ##__VA_ARGS__); break;  \
+    case FLA_F16 * 1000 + 32: e = LAUNCH<F16, 32>(ARGS, ##__VA_ARGS__); break;    \
+    case FLA_F16 * 1000 + 64: e = LAUNCH<F16, 64>(ARGS, ##__VA_ARGS__); break;    \
+    case FLA_F16 * 1000 + 128: e = LAUNCH<F16, 128>(ARGS, ##__VA_ARGS__); break;  \
+    case FLA_BF16 * 1000 + 32: e = LAUNCH<BF16, 32>(ARGS, ##__VA_ARGS__); break;  \
+    case FLA_BF16 * 1000 + 64: e = LAUNCH<BF16, 64>(ARGS, ##__VA_ARGS__); break;  \
+    case FLA_BF16 * 1000 + 128: e = LAUNCH<BF16, 128>(ARGS, ##__VA_ARGS__); break; \
+    default: return FLA_EUNSUPPORTED;                                             \
+  }
+
+extern "C" const char* fla_version(void) { return "flashlazy-gfx950 0.1.0"; }
+
+extern "C" int fla_adasplash_mask_words(int L) {
+  if (L <= 0) return 0;
+  const int tc = (L + 63) / 64;
+  return (tc + 31) / 32;
+}
+
+extern "C" int fla_adasplash_fwd(const fla_tensor4_t* q, const fla_tensor4_t* k, const fla_tensor4_t* v,
+                                 const fla_tensor4_t* out, float* tau, float* wn, uint32_t* block_mask,
+                                 const int32_t* varlen, int B, int H, int L, int D, int dtype, float alpha, int niter,
+                                 int is_causal, int skip_empty_blocks, float scale, void* stream) {
+  if (!good_common(B, H, L, D, dtype)) return FLA_EINVAL;
+  if (!good_tensor(q, dtype) || !good_tensor(k, dtype) || !good_tensor(v, dtype) || !good_tensor(out, dtype))
+    return FLA_EINVAL;
+  if (!tau || !(alpha > 1.0f) || alpha > 2.0f || !(scale > 0.0f)) return FLA_EINVAL;
+  AdaFwdArgs a;
+  a.q = T4(q);
+  a.k = T4(k);
+  a.v = T4(v);
+  a.o = T4(out);
+  a.tau = tau;
+  a.wn = wn;
+  a.mask = block_mask;
+  a.varlen = varlen;
+  a.B = B;
+  a.H = H;
+  a.L = L;
+  a.Tr = (L + 127) / 128;
+  a.MW = fla_adasplash_mask_words(L);
+  a.cz = (alpha - 1.0f) * scale;
+  a.beta = 1.0f / (alpha - 1.0f);
+  a.causal = is_causal ? 1 : 0;
+  a.skip = skip_empty_blocks ? 1 : 0;
+  a.fb_maxit = niter > 100 ? niter : 100;
+  const int mode = alpha_mode(alpha);
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e;
+  FLA_DISPATCH(ada_fwd_launch, a, mode, s)
+  return (int)e;
+}
+
+extern "C" int fla_adasplash_bwd(const fla_tensor4_t* q, const fla_tensor4_t* k, const fla_tensor4_t* v,
+                                 const fla_tensor4_t* dout, const fla_tensor4_t* dq, const fla_tensor4_t* dk,
+                                 const fla_tensor4_t* dv, const float* tau, const float* wn,
+                                 const uint32_t* block_mask, const int32_t* varlen, float* delta_ws, int B, int H,
+                                 int L, int D, int dtype, float alpha, int is_causal, float scale, void* stream) {
+  if (!good_common(B, H, L, D, dtype)) return FLA_EINVAL;
+  if (!good_tensor(q, dtype) || !good_tensor(k, dtype) || !good_tensor(v, dtype) || !good_tensor(dout, dtype) ||
+      !good_tensor(dq, dtype) || !good_tensor(dk, dtype) || !good_tensor(dv, dtype))
+    return FLA_EINVAL;
+  if (!tau || !wn || !delta_ws || !(alpha > 1.0f) || alpha > 2.0f || !(scale > 0.0f)) return FLA_EINVAL;
+  AdaBwdArgs a;
+  a.q = T4(q);
+  a.k = T4(k);
+  a.v = T4(v);
+  a.dout = T4(dout);
+  a.dq = T4(dq);
+  a.dk = T4(dk);
+  a.dv = T4(dv);
+  a.tau = tau;
+  a.wn = wn;
+  a.mask = block_mask;
+  a.varlen = varlen;
+  a.delta = delta_ws;
+  a.B = B;
+  a.H = H;
+  a.L = L;
+  a.Tr = (L + 127) / 128;
+  a.MW = fla_adasplash_mask_words(L);
+  a.cz = (alpha - 1.0f) * scale;
+  a.beta = 1.0f / (alpha - 1.0f);
+  a.scale = scale;
+  a.causal = is_causal ? 1 : 0;
+  const int mode = alpha_mode(alpha);
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e;
+  FLA_DISPATCH(ada_bwd_launch, a, mode, s)
+  return (int)e;
+}
+
+extern "C" size_t fla_lazy_bwd_workspace_size(int B, int H, int L, int window) {
+  if (B <= 0 || H <= 0 || L <= 0 || window <= 0) return 0;
+  const size_t nqt = (size_t)(L + 127) / 128;
+  const size_t parts = (size_t)B * H * nqt;
+  // dbias partials, dtau partials, delta [B, H, L]; each region 256-byte aligned.
+  auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
+  return up(parts * (size_t)window * 4) + up(parts * 4) + up((size_t)B * H * L * 4);
+}
+
+extern "C" int fla_lazy_fwd(const fla_tensor4_t* q, const fla_tensor4_t* k, const fla_tensor4_t* v,
+                            const fla_tensor4_t* out, const float* bias, int64_t bias_ld, const float* tau,
+                            int window, float* lse, float* wdelta, const int32_t* varlen, int B, int H, int L, int D,
+                            int dtype, float scale, void* stream) {
+  if (!good_common(B, H, L, D, dtype)) return FLA_EINVAL;
+  if (!good_tensor(q, dtype) || !good_tensor(k, dtype) || !good_tensor(v, dtype) || !good_tensor(out, dtype))
+    return FLA_EINVAL;
+  if (!bias || !tau || !lse || window <= 0 || bias_ld < window || !(scale > 0.0f)) return FLA_EINVAL;
+  LazyArgs a = {};
+  a.q = T4(q);
+  a.k = T4(k);
+  a.v = T4(v);
+  a.o = T4(out);
+  a.bias = bias;
+  a.bias_ld = bias_ld;
+  a.tau = tau;
+  a.lse = lse;
+  a.wdelta = wdelta;
+  a.varlen = varlen;
+  a.B = B;
+  a.H = H;
+  a.L = L;
+  a.W = window;
+  a.nQT = (L + 127) / 128;
+  a.scale = scale;
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e;
+  FLA_DISPATCH(lazy_fwd_launch, a, s)
+  return (int)e;
+}
+
+extern "C" int fla_lazy_bwd(const fla_tensor4_t* q, const fla_tensor4_t* k, const fla_tensor4_t* v,
+                            const fla_tensor4_t* dout, const fla_tensor4_t* dq, const fla_tensor4_t* dk,
+                            const fla_tensor4_t* dv, const float* bias, int64_t bias_ld, const float* tau, int window,
+                            const float* lse, const float* wdelta, const int32_t* varlen, float* dbias, float* dtau,
+                            void* workspace, size_t workspace_bytes, int B, int H, int L, int D, int dtype,
+                            float scale, void* stream) {
+  if (!good_common(B, H, L, D, dtype)) return FLA_EINVAL;
+  if (!good_tensor(q, dtype) || !good_tensor(k, dtype) || !good_tensor(v, dtype) || !good_tensor(dout, dtype) ||
+      !good_tensor(dq, dtype) || !good_tensor(dk, dtype) || !good_tensor(dv, dtype))
+    return FLA_EINVAL;
+  if (!bias || !tau || !lse || !wdelta || window <= 0 || bias_ld < window || !(scale > 0.0f)) return FLA_EINVAL;
+  if ((dbias == nullptr) != (dtau == nullptr)) return FLA_EINVAL;
+  const size_t need = fla_lazy_bwd_workspace_size(B, H, L, window);
+  if (!workspace || workspace_bytes < need || ((uintptr_t)workspace) % 256) return FLA_EWORKSPACE;
+  LazyArgs a = {};
+  a.q = T4(q);
+  a.k = T4(k);
+  a.v = T4(v);
+  a.dout = T4(dout);
+  a.dq = T4(dq);
+  a.dk = T4(dk);
+  a.dv = T4(dv);
+  a.bias = bias;
+  a.bias_ld = bias_ld;
+  a.tau = tau;
+  a.lse = const_cast<float*>(lse);
+  a.wdelta = const_cast<float*>(wdelta);
+  a.varlen = varlen;
+  a.B = B;
+  a.H = H;
+  a.L = L;
+  a.W = window;
+  a.nQT = (L + 127) / 128;
+  a.scale = scale;
+  const size_t parts = (size_t)B * H * a.nQT;
+  auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
+  char* ws = (char*)workspace;
+  a.dbias_part = (float*)ws;
+  a.dtau_part = (float*)(ws + up(parts * (size_t)window * 4));
+  a.delta = (float*)(ws + up(parts * (size_t)window * 4) + up(parts * 4));
+  a.dbias = dbias;
+  a.dtau = dtau;
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e;
+  FLA_DISPATCH(lazy_bwd_launch, a, s)
+  return (int)e;
+}

@@ -1,0 +1,57 @@
+// Kernel argument blocks and launcher declarations shared by the C ABI (api.hip)
+// and the per-dtype kernel translation units.
+#pragma once
+#include "common.h"
+
+namespace fla {
+
+struct AdaFwdArgs {
+  Tensor4 q, k, v, o;
+  float* tau;              // [B, H, L] threshold, (alpha-1)*score units
+  float* wn;               // [B, H, L, D] sum U v / sum U, optional
+  uint32_t* mask;          // [B, H, Tr, MW] block mask, optional
+  const int32_t* varlen;   // [B], optional
+  int B, H, L, Tr, MW;
+  float cz, beta;          // cz = (alpha-1)*scale, beta = 1/(alpha-1)
+  int causal, skip, fb_maxit;
+};
+
+struct AdaBwdArgs {
+  Tensor4 q, k, v, dout, dq, dk, dv;
+  const float* tau;
+  const float* wn;
+  const uint32_t* mask;
+  const int32_t* varlen;
+  float* delta;            // [B, H, L] scratch
+  int B, H, L, Tr, MW;
+  float cz, beta, scale;
+  int causal;
+};
+
+struct LazyArgs {
+  Tensor4 q, k, v, o, dout, dq, dk, dv;
+  const float* bias;       // fp32 [H, bias_ld]
+  int64_t bias_ld;
+  const float* tau;        // fp32 [H]
+  float* lse;              // [B, H, L]
+  float* wdelta;           // [B, H, L, D], optional
+  float* delta;            // [B, H, L] scratch (backward)
+  const int32_t* varlen;
+  float* dbias_part;       // [B*H*nQT, window] per-tile partials (backward, optional)
+  float* dtau_part;        // [B*H*nQT]
+  float* dbias;            // [H, window]
+  float* dtau;             // [H]
+  int B, H, L, W, nQT;
+  float scale;
+};
+
+template <int DT, int D>
+hipError_t ada_fwd_launch(const AdaFwdArgs& a, int mode, hipStream_t s);
+template <int DT, int D>
+hipError_t ada_bwd_launch(const AdaBwdArgs& a, int mode, hipStream_t s);
+template <int DT, int D>
+hipError_t lazy_fwd_launch(const LazyArgs& a, hipStream_t s);
+template <int DT, int D>
+hipError_t lazy_bwd_launch(const LazyArgs& a, hipStream_t s);
+
+}  // namespace fla

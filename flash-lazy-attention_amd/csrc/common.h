@@ -1,0 +1,244 @@
+// Shared device helpers for the gfx950 (MI355X, CDNA4) kernels of this library.
+//
+// Conventions used by every attention kernel:
+//  * wave64; a 256-thread workgroup is 4 waves.
+//  * Matrix products use the 32x32 MFMA family.  For C[32][32] += A[32][K] B[K][32]
+//    lane l supplies row (l%32) of A and column (l%32) of B, each as KPL consecutive
+//    "k slots", and lane group g = l/32 selects which slots.  The accumulator holds
+//    column (l%32) and the 16 rows  row_of(r, g) = 8*(r/4) + 4*g + (r%4),  r = 0..15.
+//  * When an accumulator is fed back as the B operand of the next product (P^T, dS^T ...)
+//    the contraction index of register r is row_of(r, g).  The A operand of that product
+//    is then read with the same mapping, so the pairing of k slots between A and B is a
+//    permutation shared by both operands and the sum over k is unchanged.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fla {
+
+enum DType : int { F32 = 0, F16 = 1, BF16 = 2 };
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ constexpr int row_of(int r, int g) { return 8 * (r >> 2) + 4 * g + (r & 3); }
+
+// Element type traits: storage type, MFMA fragment type, k slots per lane.
+template <int DT>
+struct Tr;
+
+template <>
+struct Tr<BF16> {
+  typedef uint16_t T;
+  typedef bf16x8 frag;
+  static constexpr int KPL = 8;
+  static __device__ __forceinline__ f32x16 mma(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ float to_f(T x) { return __uint_as_float(((uint32_t)x) << 16); }
+  static __device__ __forceinline__ T from_f(float x) {
+    __bf16 h = (__bf16)x;
+    return __builtin_bit_cast(uint16_t, h);
+  }
+  static __device__ __forceinline__ void set(frag& f, int e, float x) { f[e] = (__bf16)x; }
+  static __device__ __forceinline__ void set_raw(frag& f, int e, T x) { f[e] = __builtin_bit_cast(__bf16, x); }
+  static __device__ __forceinline__ frag zero() { frag f; for (int e = 0; e < 8; ++e) f[e] = (__bf16)0.0f; return f; }
+};
+
+template <>
+struct Tr<F16> {
+  typedef uint16_t T;
+  typedef f16x8 frag;
+  static constexpr int KPL = 8;
+  static __device__ __forceinline__ f32x16 mma(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ float to_f(T x) { return (float)__builtin_bit_cast(_Float16, x); }
+  static __device__ __forceinline__ T from_f(float x) { return __builtin_bit_cast(uint16_t, (_Float16)x); }
+  static __device__ __forceinline__ void set(frag& f, int e, float x) { f[e] = (_Float16)x; }
+  static __device__ __forceinline__ void set_raw(frag& f, int e, T x) { f[e] = __builtin_bit_cast(_Float16, x); }
+  static __device__ __forceinline__ frag zero() { frag f; for (int e = 0; e < 8; ++e) f[e] = (_Float16)0.0f; return f; }
+};
+
+template <>
+struct Tr<F32> {
+  typedef float T;
+  typedef float frag;
+  static constexpr int KPL = 1;
+  static __device__ __forceinline__ f32x16 mma(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ float to_f(T x) { return x; }
+  static __device__ __forceinline__ T from_f(float x) { return x; }
+  static __device__ __forceinline__ void set(frag& f, int, float x) { f = x; }
+  static __device__ __forceinline__ void set_raw(frag& f, int, T x) { f = x; }
+  static __device__ __forceinline__ frag zero() { return 0.0f; }
+};
+
+// Load KPL consecutive elements (16 bytes for 16-bit types) as one fragment.
+template <int DT>
+__device__ __forceinline__ typename Tr<DT>::frag load_frag(const typename Tr<DT>::T* p) {
+  return *reinterpret_cast<const typename Tr<DT>::frag*>(p);
+}
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+  for (int i = 0; i < 16; ++i) z[i] = 0.0f;
+  return z;
+}
+
+// Cross-lane helpers (wave64).
+__device__ __forceinline__ float pair_sum(float x) { return x + __shfl_xor(x, 32); }
+__device__ __forceinline__ float pair_max(float x) { return fmaxf(x, __shfl_xor(x, 32)); }
+__device__ __forceinline__ float pair_min(float x) { return fminf(x, __shfl_xor(x, 32)); }
+
+__device__ __forceinline__ float wave_sum(float x) {
+  for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m);
+  return x;
+}
+__device__ __forceinline__ float wave_max(float x) {
+  for (int m = 32; m >= 1; m >>= 1) x = fmaxf(x, __shfl_xor(x, m));
+  return x;
+}
+__device__ __forceinline__ float wave_min(float x) {
+  for (int m = 32; m >= 1; m >>= 1) x = fminf(x, __shfl_xor(x, m));
+  return x;
+}
+
+// t^beta and t^(beta-1) for t > 0.  MODE 1: alpha = 1.5 (beta = 2), MODE 2: alpha = 2
+// (beta = 1), MODE 0: any alpha in (1, 2] via exp2/log2.
+template <int MODE>
+__device__ __forceinline__ void pow_pair(float t, float beta, float& p, float& u) {
+  if (MODE == 1) {
+    p = t * t;
+    u = t;
+  } else if (MODE == 2) {
+    p = t;
+    u = 1.0f;
+  } else {
+    float lg = __builtin_amdgcn_logf(t);  // log2
+    u = __builtin_amdgcn_exp2f((beta - 1.0f) * lg);
+    p = u * t;
+  }
+}
+
+// Threshold solver step shared by every entmax kernel.  In z = (alpha-1)*score units
+// f(tau) = sum_j [z_j - tau]_+^beta - 1 is convex and decreasing, so Newton steps from
+// below the root never overshoot; for alpha = 1.5 / 2 the closed-form root on the current
+// support is exact once it keeps every support element positive.
+template <int MODE>
+struct RowStep {
+  // One solver step from sums over t = z - tau > 0: F = sum t^beta, G = sum t^(beta-1),
+  // K = count, tmin = smallest positive t.  Returns the step; sets `exact` when
+  // tau + step is the exact root (MODE 1/2).
+  static __device__ __forceinline__ float step(float F, float G, float K, float tmin, float beta, bool& exact) {
+    exact = false;
+    if (MODE == 1) {
+      // sum_S (t - d)^2 = 1  ->  K d^2 - 2 G d + F - 1 = 0, smaller root.
+      float disc = fmaxf(G * G - K * (F - 1.0f), 0.0f);
+      float d = (F - 1.0f) / (G + sqrtf(disc));
+      if (d < tmin) { exact = true; return d; }
+      return (F - 1.0f) / (2.0f * G);
+    } else if (MODE == 2) {
+      float d = (F - 1.0f) / K;
+      if (d < tmin) exact = true;
+      return d;
+    } else {
+      return (F - 1.0f) / (beta * G);
+    }
+  }
+};
+
+// Stage a [ROWS][D] tile of T (global row stride `ld`, rows >= nvalid zero-filled)
+// into LDS with row stride LDR elements.  16-byte vector moves, all 256 threads.
+template <typename T, int ROWS, int D, int LDR>
+__device__ __forceinline__ void stage_rows(T* __restrict__ lds, const T* __restrict__ g, int64_t ld, int nvalid, int tid) {
+  constexpr int EPV = 16 / sizeof(T);
+  constexpr int CPR = D / EPV;
+  constexpr int NCH = ROWS * CPR;
+#pragma unroll
+  for (int c = tid; c < NCH; c += 256) {
+    int row = c / CPR, col = (c % CPR) * EPV;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (row < nvalid) v = *reinterpret_cast<const uint4*>(g + row * ld + col);
+    *reinterpret_cast<uint4*>(lds + row * LDR + col) = v;
+  }
+}
+
+// Stage a [ROWS][D] global tile transposed into LDS as [D][ROWS] with row stride LDR.
+template <typename T, int ROWS, int D, int LDR>
+__device__ __forceinline__ void stage_rows_t(T* __restrict__ lds, const T* __restrict__ g, int64_t ld, int nvalid, int tid) {
+  constexpr int EPV = 16 / sizeof(T);
+  constexpr int CPR = D / EPV;
+  constexpr int NCH = ROWS * CPR;
+#pragma unroll
+  for (int c = tid; c < NCH; c += 256) {
+    int row = c % ROWS, col = (c / ROWS) * EPV;
+    union { uint4 v; T e[EPV]; } u;
+    u.v = make_uint4(0, 0, 0, 0);
+    if (row < nvalid) u.v = *reinterpret_cast<const uint4*>(g + row * ld + col);
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) lds[(col + e) * LDR + row] = u.e[e];
+  }
+}
+
+// t = (alpha-1)*scale*s - tau with the product rounded before the subtraction, so every
+// kernel that decides p > 0 makes the same decision for the same score.
+__device__ __forceinline__ float zt(float s, float cz, float tau) {
+#pragma clang fp contract(off)
+  float z = s * cz;
+  return z - tau;
+}
+
+// A fragment whose contraction index runs along a contiguous LDS row, with the k slots
+// paired to accumulator registers (row_of mapping).  `row` points at the first key of a
+// 32-key block; j is the instruction index inside the block.
+template <int DT>
+__device__ __forceinline__ typename Tr<DT>::frag load_perm_frag(const typename Tr<DT>::T* row, int j, int g) {
+  typedef typename Tr<DT>::frag frag;
+  if constexpr (Tr<DT>::KPL == 8) {
+    uint2 lo = *reinterpret_cast<const uint2*>(row + 16 * j + 4 * g);
+    uint2 hi = *reinterpret_cast<const uint2*>(row + 16 * j + 8 + 4 * g);
+    uint4 w = make_uint4(lo.x, lo.y, hi.x, hi.y);
+    return __builtin_bit_cast(frag, w);
+  } else {
+    return row[row_of(j, g)];
+  }
+}
+
+// B fragment from accumulator values (registers j*KPL .. j*KPL+KPL-1).
+template <int DT>
+__device__ __forceinline__ typename Tr<DT>::frag acc_frag(const f32x16& a, int j) {
+  typename Tr<DT>::frag f;
+#pragma unroll
+  for (int e = 0; e < Tr<DT>::KPL; ++e) Tr<DT>::set(f, e, a[j * Tr<DT>::KPL + e]);
+  return f;
+}
+
+// Store a transposed accumulator block (lane = row `row`, registers = 16 columns of a
+// 32-wide column block `d`) into a row-major [.., D] T tensor, scaled.
+template <int DT>
+__device__ __forceinline__ void store_acc_row(typename Tr<DT>::T* rowp, const f32x16& acc, int dblk, int g, float sc) {
+  typedef typename Tr<DT>::T T;
+#pragma unroll
+  for (int r4 = 0; r4 < 4; ++r4) {
+    const int d0 = dblk * 32 + 8 * r4 + 4 * g;
+    if constexpr (sizeof(T) == 2) {
+      uint32_t w0 = (uint32_t)Tr<DT>::from_f(acc[4 * r4] * sc) | ((uint32_t)Tr<DT>::from_f(acc[4 * r4 + 1] * sc) << 16);
+      uint32_t w1 = (uint32_t)Tr<DT>::from_f(acc[4 * r4 + 2] * sc) | ((uint32_t)Tr<DT>::from_f(acc[4 * r4 + 3] * sc) << 16);
+      *reinterpret_cast<uint2*>(rowp + d0) = make_uint2(w0, w1);
+    } else {
+      *reinterpret_cast<float4*>(rowp + d0) =
+          make_float4(acc[4 * r4] * sc, acc[4 * r4 + 1] * sc, acc[4 * r4 + 2] * sc, acc[4 * r4 + 3] * sc);
+    }
+  }
+}
+
+struct Tensor4 {
+  void* data;
+  int64_t sb, sh, sl;  // element strides of the B, H, L dims; the D dim is contiguous
+};
+
+}  // namespace fla

@@ -1,0 +1,113 @@
+/*
+ * flashlazy.h -- C ABI of the MI355X (gfx950) AdaSplash / Lazy-Attention kernels.
+ *
+ * Every entry point takes raw device pointers, sizes and element strides, allocates
+ * nothing, launches asynchronously on the caller's HIP stream (passed as `void*`,
+ * a hipStream_t; NULL = default stream) and returns 0 on success, a negative
+ * FLA_E* code for rejected arguments, or a positive hipError_t from the launch.
+ *
+ * Tensors of shape [B, H, L, D] are described by fla_tensor4_t: a data pointer and
+ * the element strides of the B, H and L dimensions; the D dimension must be
+ * contiguous and rows must be 16-byte aligned.  dtype is one of FLA_F32, FLA_F16,
+ * FLA_BF16; D must be 32, 64 or 128 (callers pad smaller head dims with zeros and
+ * pass the softmax scale of the true head dim).
+ */
+#ifndef FLASHLAZY_H
+#define FLASHLAZY_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FLA_OK 0
+#define FLA_EINVAL (-1)
+#define FLA_EUNSUPPORTED (-2)
+#define FLA_EWORKSPACE (-3)
+
+enum { FLA_F32 = 0, FLA_F16 = 1, FLA_BF16 = 2 };
+
+typedef struct {
+  void* data;
+  int64_t stride_b, stride_h, stride_l;
+} fla_tensor4_t;
+
+/* Library version string. */
+const char* fla_version(void);
+
+/* Row-wise alpha-entmax over the last dimension of a [rows, n] matrix (row strides
+ * ldx / ldy in elements).  Replaces the kernel behind
+ * `adasplash.triton_entmax(x, alpha, n_iter, fast_math)` (reference README.md:28-35;
+ * tests/test_triton_entmax.py).  1 < alpha <= 2.  The threshold is solved to fp32
+ * convergence; n_iter only raises the iteration cap. */
+int fla_entmax_fwd(const void* x, void* y, int64_t rows, int64_t n, int64_t ldx, int64_t ldy, int dtype, float alpha,
+                   int n_iter, int fast_math, void* stream);
+
+/* Backward of fla_entmax_fwd given its output y: dx = U dy - (sum U dy / sum U) U,
+ * U = y^(2-alpha) on y > 0 (autograd backward of `triton_entmax`, gradcheck at
+ * tests/test_triton_entmax.py:33-41). */
+int fla_entmax_bwd(const void* y, const void* dy, void* dx, int64_t rows, int64_t n, int64_t ldy, int64_t lddy,
+                   int64_t lddx, int dtype, float alpha, void* stream);
+
+/* Number of uint32 words per query-tile row of the AdaSplash block mask
+ * (ceil(ceil(L/64)/32)).  The mask is [B, H, ceil(L/128), words]: bit c%32 of word
+ * c/32 in row r is set iff some query i < varlen of tile r (rows 128r..128r+127) has
+ * p_ij > 0 for a key j of tile c (keys 64c..64c+63). */
+int fla_adasplash_mask_words(int L);
+
+/* AdaSplash forward: out = entmax_alpha(q k^T * scale, masked) v.
+ * Replaces `adasplash(q, k, v, alpha, niter, is_causal, varlen)` (block-masked,
+ * skip_empty_blocks = 1, block_mask written) and `adasplash_no_block_mask(...)`
+ * (skip_empty_blocks = 0, block_mask may be NULL) -- reference README.md:39-58,
+ * tests/test_adasplash.py, tests/test_adasplash_no_block_mask.py.
+ *   tau  [B, H, L] fp32 out: threshold in (alpha-1)*score units, +inf on rows >= varlen.
+ *   wn   [B, H, L, D] fp32 out, optional (needed by the backward):
+ *        sum_j U_ij v_j / sum_j U_ij with U = p^(2-alpha).
+ *   varlen [B] int32, optional: keys j >= varlen[b] are masked, output rows >= varlen[b] are zero.
+ * niter is accepted for signature compatibility; the threshold is solved to fp32
+ * convergence (niter raises the cap of the full-sweep fallback). */
+int fla_adasplash_fwd(const fla_tensor4_t* q, const fla_tensor4_t* k, const fla_tensor4_t* v,
+                      const fla_tensor4_t* out, float* tau, float* wn, uint32_t* block_mask, const int32_t* varlen,
+                      int B, int H, int L, int D, int dtype, float alpha, int niter, int is_causal,
+                      int skip_empty_blocks, float scale, void* stream);
+
+/* AdaSplash backward (dq, dk, dv) through the entmax Jacobian, from the forward's
+ * tau and wn.  block_mask (optional) makes both backward kernels skip empty tiles.
+ * delta_ws: caller-provided [B, H, L] fp32 scratch. */
+int fla_adasplash_bwd(const fla_tensor4_t* q, const fla_tensor4_t* k, const fla_tensor4_t* v,
+                      const fla_tensor4_t* dout, const fla_tensor4_t* dq, const fla_tensor4_t* dk,
+                      const fla_tensor4_t* dv, const float* tau, const float* wn, const uint32_t* block_mask,
+                      const int32_t* varlen, float* delta_ws, int B, int H, int L, int D, int dtype, float alpha,
+                      int is_causal, float scale, void* stream);
+
+/* Lazy attention forward: causal elastic softmax relu(softmax(q k^T*scale + bias) + tau_h/(i+1)) v
+ * with bias[h, i-j] added for 0 <= i-j < window.  Replaces `lazy_attention_triton`'s
+ * forward (reference lazy_attention_triton.py:503-515, 543-583; kernels :9-174).
+ *   bias fp32 [H, >= window] with row stride bias_ld; tau fp32 [H].
+ *   lse [B, H, L] fp32 out (log-sum-exp of the scores, natural log).
+ *   wdelta [B, H, L, D] fp32 out, optional (needed by the backward):
+ *          sum_j 1[p_ij + tau/(i+1) > 0] p_ij v_j.
+ *   varlen [B] int32, optional. */
+int fla_lazy_fwd(const fla_tensor4_t* q, const fla_tensor4_t* k, const fla_tensor4_t* v, const fla_tensor4_t* out,
+                 const float* bias, int64_t bias_ld, const float* tau, int window, float* lse, float* wdelta,
+                 const int32_t* varlen, int B, int H, int L, int D, int dtype, float scale, void* stream);
+
+/* Bytes of caller-provided scratch that fla_lazy_bwd needs (per-tile dbias / dtau partials). */
+size_t fla_lazy_bwd_workspace_size(int B, int H, int L, int window);
+
+/* Lazy attention backward (reference lazy_attention_triton.py:518-541, 585-745; kernels :180-497).
+ * dbias fp32 [H, window] and dtau fp32 [H] are optional (NULL = frozen parameters, the
+ * reference's `_lazy_attention_backward_fast` path). */
+int fla_lazy_bwd(const fla_tensor4_t* q, const fla_tensor4_t* k, const fla_tensor4_t* v, const fla_tensor4_t* dout,
+                 const fla_tensor4_t* dq, const fla_tensor4_t* dk, const fla_tensor4_t* dv, const float* bias,
+                 int64_t bias_ld, const float* tau, int window, const float* lse, const float* wdelta,
+                 const int32_t* varlen, float* dbias, float* dtau, void* workspace, size_t workspace_bytes, int B,
+                 int H, int L, int D, int dtype, float scale, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLASHLAZY_H */

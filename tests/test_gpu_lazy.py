@@ -1,0 +1,129 @@
+"""lazy_attention_triton on the GPU vs the oracle.
+
+Mirrors tests/test_lazy_attention_triton.py, tests/test_lazy_attention_triton_backward.py and
+tests/test_lazy_attention_varlen.py; the bias window follows the kernel (0 <= i-j < W,
+lazy_attention_triton.py:62).
+"""
+import numpy as np
+import pytest
+import torch
+
+from _gpu_util import DEV, assert_close, banner, rand, to_np
+from oracle.lazy import lazy_backward, lazy_forward
+
+pytestmark = pytest.mark.gpu
+
+
+def _op():
+    from adasplash import lazy_attention_triton
+
+    return lazy_attention_triton
+
+
+def _case(B, H, L, D, Wb, dtype, seed=42, tau=-1.0):
+    q, k, v = (rand((B, H, L, D), dtype, seed + i) for i in range(3))
+    bias = rand((H, Wb), torch.float32, seed + 3)
+    t = torch.full((H,), tau, dtype=torch.float32)
+    return q, k, v, bias, t
+
+
+def test_forward_vs_reference_fp32():
+    # tests/test_lazy_attention_triton.py:16-90 (B2 H4 L128 D64, W=32, bias [H, W+1])
+    q, k, v, bias, tau = _case(2, 4, 128, 64, 33, torch.float32)
+    ref = lazy_forward(to_np(q), to_np(k), to_np(v), to_np(bias), to_np(tau), 32)
+    out = _op()(q.to(DEV), k.to(DEV), v.to(DEV), bias.to(DEV), tau.to(DEV), window_size=32)
+    assert_close(to_np(out), ref, 1e-5, "lazy forward")
+
+
+@pytest.mark.parametrize("tauval", [-1.0, -0.2, 0.3])
+@pytest.mark.parametrize("shape", [(1, 1, 32, 16, 8), (2, 2, 200, 64, 48), (1, 2, 300, 32, 500)])
+def test_backward_vs_reference_fp32(tauval, shape):
+    # tests/test_lazy_attention_triton_backward.py:40-111 (B1 H1 L32 D16 W8)
+    B, H, L, D, W = shape
+    banner("lazy bwd fp32", shape, tauval)
+    q, k, v, bias, tau = _case(B, H, L, D, W + 1, torch.float32, seed=5, tau=tauval)
+    do = rand((B, H, L, D), torch.float32, 77)
+    ref_out = lazy_forward(to_np(q), to_np(k), to_np(v), to_np(bias), to_np(tau), W)
+    ref = lazy_backward(to_np(q), to_np(k), to_np(v), to_np(bias), to_np(tau), to_np(do), W)
+    ts = [t.to(DEV).requires_grad_(True) for t in (q, k, v, bias, tau)]
+    out = _op()(*ts, window_size=W)
+    assert_close(to_np(out), ref_out, 1e-5, "forward")
+    out.backward(do.to(DEV))
+    for got, r, n in zip([t.grad for t in ts], ref, ["dq", "dk", "dv", "dbias", "dtau"]):
+        assert_close(to_np(got), r, 1e-4 * max(1.0, np.abs(r).max()), n)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_lowp_forward_backward(dtype):
+    banner("lazy lowp", dtype)
+    B, H, L, D, W = 2, 2, 384, 64, 96
+    q, k, v, bias, tau = _case(B, H, L, D, W, dtype, seed=9)
+    bias = bias * 0.5
+    do = rand((B, H, L, D), dtype, 10)
+    ref_out = lazy_forward(to_np(q), to_np(k), to_np(v), to_np(bias), to_np(tau), W)
+    ref = lazy_backward(to_np(q), to_np(k), to_np(v), to_np(bias), to_np(tau), to_np(do), W)
+    ts = [q.to(DEV).requires_grad_(True), k.to(DEV).requires_grad_(True), v.to(DEV).requires_grad_(True),
+          bias.to(DEV).requires_grad_(True), tau.to(DEV).requires_grad_(True)]
+    out = _op()(*ts)
+    assert_close(to_np(out), ref_out, 2e-2, "forward")
+    out.backward(do.to(DEV))
+    for got, r, n in zip([t.grad for t in ts], ref, ["dq", "dk", "dv", "dbias", "dtau"]):
+        assert_close(to_np(got), r, 2e-2 * max(1.0, np.abs(r).max() / 2), n)
+
+
+def test_varlen_forward_and_padding():
+    # tests/test_lazy_attention_varlen.py:13-134
+    q, k, v, bias, tau = _case(2, 4, 128, 64, 33, torch.float32, seed=1)
+    varlen = torch.tensor([64, 100], dtype=torch.int32)
+    ref = lazy_forward(to_np(q), to_np(k), to_np(v), to_np(bias), to_np(tau), 32, varlen.numpy())
+    out = _op()(q.to(DEV), k.to(DEV), v.to(DEV), bias.to(DEV), tau.to(DEV), window_size=32, varlen=varlen.to(DEV))
+    assert (out[0, :, 64:] == 0).all() and (out[1, :, 100:] == 0).all()
+    assert_close(to_np(out), ref, 1e-5, "varlen forward")
+
+
+@pytest.mark.parametrize("tauval", [-1.0, 0.4])
+def test_varlen_backward(tauval):
+    # tests/test_lazy_attention_varlen.py:136-169 (+ values vs the oracle)
+    B, H, L, D, W = 2, 4, 64, 32, 16
+    q, k, v, bias, tau = _case(B, H, L, D, W, torch.float32, seed=2, tau=tauval)
+    varlen = np.array([32, 48])
+    do = rand((B, H, L, D), torch.float32, 3)
+    ref = lazy_backward(to_np(q), to_np(k), to_np(v), to_np(bias), to_np(tau), to_np(do), W, varlen)
+    ts = [t.to(DEV).requires_grad_(True) for t in (q, k, v, bias, tau)]
+    out = _op()(*ts, window_size=W, varlen=torch.tensor(varlen, dtype=torch.int32, device=DEV))
+    out.backward(do.to(DEV))
+    for got, r, n in zip([t.grad for t in ts], ref, ["dq", "dk", "dv", "dbias", "dtau"]):
+        assert_close(to_np(got), r, 1e-4 * max(1.0, np.abs(r).max()), n)
+    for t in ts[:3]:
+        assert (t.grad[0, :, 32:] == 0).all() and (t.grad[1, :, 48:] == 0).all()
+
+
+def test_frozen_parameters_fast_path():
+    q, k, v, bias, tau = _case(1, 2, 96, 64, 16, torch.float32, seed=4)
+    do = rand((1, 2, 96, 64), torch.float32, 5)
+    ref = lazy_backward(to_np(q), to_np(k), to_np(v), to_np(bias), to_np(tau), to_np(do), 16)
+    qd, kd, vd = (t.to(DEV).requires_grad_(True) for t in (q, k, v))
+    b, t = bias.to(DEV), tau.to(DEV)
+    out = _op()(qd, kd, vd, b, t)
+    out.backward(do.to(DEV))
+    assert b.grad is None and t.grad is None
+    for got, r, n in zip((qd.grad, kd.grad, vd.grad), ref[:3], "qkv"):
+        assert_close(to_np(got), r, 1e-4, "d" + n)
+
+
+def test_very_negative_tau_gives_zero():
+    q, k, v, bias, tau = _case(1, 2, 64, 32, 8, torch.float32, seed=6, tau=-100.0)
+    out = _op()(q.to(DEV), k.to(DEV), v.to(DEV), bias.to(DEV), tau.to(DEV))
+    assert out.abs().max().item() < 1e-6
+
+
+def test_bf16_bias_and_tau_dtypes():
+    # examples pass bias / tau in the model dtype (lazy_attention_layer.py:164-170)
+    q, k, v, bias, tau = _case(1, 2, 128, 64, 32, torch.bfloat16, seed=8)
+    bb, tb = bias.to(torch.bfloat16), tau.to(torch.bfloat16)
+    ref = lazy_forward(to_np(q), to_np(k), to_np(v), to_np(bb), to_np(tb), 32)
+    ts = [t.to(DEV).requires_grad_(True) for t in (q, k, v, bb, tb)]
+    out = _op()(*ts)
+    assert_close(to_np(out), ref, 2e-2, "bf16 params forward")
+    out.sum().backward()
+    assert ts[3].grad.dtype == torch.bfloat16 and ts[4].grad.dtype == torch.bfloat16
