@@ -184,13 +184,90 @@ __device__ __forceinline__ void stage_rows_t(T* __restrict__ lds, const T* __res
   }
 }
 
-// t = (alpha-1)*scale*s - tau with the product rounded before the subtraction, so every
-// kernel that decides p > 0 makes the same decision for the same score.
-__device__ __forceinline__ float zt(float s, float cz, float tau) {
-#pragma clang fp contract(off)
-  float z = s * cz;
-  return z - tau;
-}
+// t = (alpha-1)*scale*s - tau as one fused multiply-add.  Every kernel that decides
+// p > 0 uses this same expression, so they agree on the support for the same score.
+__device__ __forceinline__ float zt(float s, float cz, float tau) { return __builtin_fmaf(s, cz, -tau); }
+
+// Register-staged tiles for software pipelining: load() issues the global reads of the next
+// tile into registers (rows >= nvalid read as zero), store() writes them to LDS later.
+template <typename T, int ROWS, int D, int LDR>
+struct RowTile {
+  static constexpr int EPV = 16 / sizeof(T);
+  static constexpr int CPR = D / EPV;
+  static constexpr int NCH = ROWS * CPR;
+  static constexpr int PER = (NCH + 255) / 256;
+  uint4 r[PER];
+  __device__ __forceinline__ void load(const T* __restrict__ g, int64_t ld, int nvalid, int tid) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int c = tid + 256 * i;
+      const int row = c / CPR, col = (c % CPR) * EPV;
+      r[i] = make_uint4(0, 0, 0, 0);
+      if (c < NCH && row < nvalid) r[i] = *reinterpret_cast<const uint4*>(g + row * ld + col);
+    }
+  }
+  __device__ __forceinline__ void store(T* __restrict__ lds, int tid) const {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int c = tid + 256 * i;
+      const int row = c / CPR, col = (c % CPR) * EPV;
+      if (c < NCH) *reinterpret_cast<uint4*>(lds + row * LDR + col) = r[i];
+    }
+  }
+};
+
+// Same, stored transposed as [D][ROWS] (row stride LDT).  16-bit types move two source rows
+// per thread so every LDS write is a packed 32-bit (row, row+1) pair.
+template <typename T, int ROWS, int D, int LDT>
+struct TransTile {
+  static constexpr int EPV = 16 / sizeof(T);
+  static constexpr int CPR = D / EPV;
+  static constexpr bool PAIR = sizeof(T) == 2;
+  static constexpr int NU = PAIR ? (ROWS / 2) * CPR : ROWS * CPR;
+  static constexpr int PER = (NU + 255) / 256;
+  uint4 r0[PER], r1[PAIR ? PER : 1];
+  __device__ __forceinline__ void load(const T* __restrict__ g, int64_t ld, int nvalid, int tid) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int u = tid + 256 * i;
+      r0[i] = make_uint4(0, 0, 0, 0);
+      if constexpr (PAIR) {
+        r1[i] = make_uint4(0, 0, 0, 0);
+        const int kp = u % (ROWS / 2), col = (u / (ROWS / 2)) * EPV;
+        if (u < NU && 2 * kp < nvalid) r0[i] = *reinterpret_cast<const uint4*>(g + (2 * kp) * ld + col);
+        if (u < NU && 2 * kp + 1 < nvalid) r1[i] = *reinterpret_cast<const uint4*>(g + (2 * kp + 1) * ld + col);
+      } else {
+        const int row = u % ROWS, col = (u / ROWS) * EPV;
+        if (u < NU && row < nvalid) r0[i] = *reinterpret_cast<const uint4*>(g + row * ld + col);
+      }
+    }
+  }
+  __device__ __forceinline__ void store(T* __restrict__ lds, int tid) const {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int u = tid + 256 * i;
+      if (u >= NU) continue;
+      if constexpr (PAIR) {
+        const int kp = u % (ROWS / 2), col = (u / (ROWS / 2)) * EPV;
+        const uint32_t a[4] = {r0[i].x, r0[i].y, r0[i].z, r0[i].w};
+        const uint32_t b[4] = {r1[i].x, r1[i].y, r1[i].z, r1[i].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          uint32_t lo = (a[e] & 0xffffu) | (b[e] << 16);
+          uint32_t hi = (a[e] >> 16) | (b[e] & 0xffff0000u);
+          *reinterpret_cast<uint32_t*>(lds + (col + 2 * e) * LDT + 2 * kp) = lo;
+          *reinterpret_cast<uint32_t*>(lds + (col + 2 * e + 1) * LDT + 2 * kp) = hi;
+        }
+      } else {
+        const int row = u % ROWS, col = (u / ROWS) * EPV;
+        const float v[4] = {__uint_as_float(r0[i].x), __uint_as_float(r0[i].y), __uint_as_float(r0[i].z),
+                            __uint_as_float(r0[i].w)};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) reinterpret_cast<float*>(lds)[(col + e) * LDT + row] = v[e];
+      }
+    }
+  }
+};
 
 // A fragment whose contraction index runs along a contiguous LDS row, with the k slots
 // paired to accumulator registers (row_of mapping).  `row` points at the first key of a

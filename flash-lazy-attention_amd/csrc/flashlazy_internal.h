@@ -3,7 +3,7 @@
 #include <hip/hip_runtime.h>
 #include <math.h>
 
-#include "../../include/flashlazy.h"
+#include "flashlazy.h"
 
 namespace fla {
 
