@@ -313,6 +313,14 @@ __device__ __forceinline__ void store_acc_row(typename Tr<DT>::T* rowp, const f3
   }
 }
 
+// LDS available to one workgroup on gfx950, and the waves-per-SIMD target of the main
+// kernels (16-bit inputs fit two workgroups per CU; fp32 tiles need the whole register file).
+static constexpr int LDS_LIMIT = 160 * 1024;
+template <int DT>
+struct Occ {
+  static constexpr int value = DT == F32 ? 1 : 2;
+};
+
 struct Tensor4 {
   void* data;
   int64_t sb, sh, sl;  // element strides of the B, H, L dims; the D dim is contiguous
