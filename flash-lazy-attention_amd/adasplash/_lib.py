@@ -107,6 +107,7 @@ def _aligned(x):
         x.stride(-1) == 1
         and x.data_ptr() % 16 == 0
         and all((s * es) % 16 == 0 for s in x.stride()[:-1])
+        and 0 < x.stride(-2) * es <= (1 << 24)
     )
 
 

@@ -15,6 +15,8 @@ bool good_tensor(const fla_tensor4_t* t, int dtype) {
   const int es = elem_size(dtype);
   if (((uintptr_t)t->data) % 16) return false;
   if ((t->stride_b * es) % 16 || (t->stride_h * es) % 16 || (t->stride_l * es) % 16) return false;
+  // tiles are read with 32-bit buffer offsets: 64 rows of stride_l must stay far below 2 GiB
+  if (t->stride_l <= 0 || t->stride_l * es > (1 << 24)) return false;
   return true;
 }
 

@@ -188,8 +188,25 @@ __device__ __forceinline__ void stage_rows_t(T* __restrict__ lds, const T* __res
 // p > 0 uses this same expression, so they agree on the support for the same score.
 __device__ __forceinline__ float zt(float s, float cz, float tau) { return __builtin_fmaf(s, cz, -tau); }
 
-// Register-staged tiles for software pipelining: load() issues the global reads of the next
-// tile into registers (rows >= nvalid read as zero), store() writes them to LDS later.
+// Buffer resource over [base, base + bytes): raw buffer loads past the end return zero, which
+// zero-fills tile rows beyond the valid sequence length without any per-lane test.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+// Bytes covering rows [0, nvalid) of a tile with row stride ld and D columns.
+template <typename T, int D>
+__device__ __forceinline__ uint32_t tile_bytes(int64_t ld, int nvalid) {
+  return nvalid > 0 ? (uint32_t)(((int64_t)(nvalid - 1) * ld + D) * sizeof(T)) : 0u;
+}
+
+// Register-staged tiles for software pipelining: init() fixes each thread's byte offsets once,
+// load() issues the global reads of a tile into registers (rows >= nvalid read as zero),
+// store() writes them to LDS later.
 template <typename T, int ROWS, int D, int LDR>
 struct RowTile {
   static constexpr int EPV = 16 / sizeof(T);
@@ -197,14 +214,20 @@ struct RowTile {
   static constexpr int NCH = ROWS * CPR;
   static constexpr int PER = (NCH + 255) / 256;
   uint4 r[PER];
-  __device__ __forceinline__ void load(const T* __restrict__ g, int64_t ld, int nvalid, int tid) {
+  uint32_t off[PER];
+  __device__ __forceinline__ void init(int64_t ld, int tid) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int c = tid + 256 * i;
       const int row = c / CPR, col = (c % CPR) * EPV;
-      r[i] = make_uint4(0, 0, 0, 0);
-      if (c < NCH && row < nvalid) r[i] = *reinterpret_cast<const uint4*>(g + row * ld + col);
+      off[i] = (uint32_t)(((int64_t)row * ld + col) * sizeof(T));
     }
+  }
+  __device__ __forceinline__ void load(const T* __restrict__ g, int64_t ld, int nvalid, int tid) {
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(g, tile_bytes<T, D>(ld, min(nvalid, ROWS)));
+#pragma unroll
+    for (int i = 0; i < PER; ++i)
+      if (tid + 256 * i < NCH) r[i] = buf_load16(rs, off[i]);
   }
   __device__ __forceinline__ void store(T* __restrict__ lds, int tid) const {
 #pragma unroll
@@ -217,7 +240,7 @@ struct RowTile {
 };
 
 // Same, stored transposed as [D][ROWS] (row stride LDT).  16-bit types move two source rows
-// per thread so every LDS write is a packed 32-bit (row, row+1) pair.
+// per thread so every LDS write is one packed 32-bit (row, row+1) pair (one v_perm_b32 each).
 template <typename T, int ROWS, int D, int LDT>
 struct TransTile {
   static constexpr int EPV = 16 / sizeof(T);
@@ -226,20 +249,30 @@ struct TransTile {
   static constexpr int NU = PAIR ? (ROWS / 2) * CPR : ROWS * CPR;
   static constexpr int PER = (NU + 255) / 256;
   uint4 r0[PER], r1[PAIR ? PER : 1];
-  __device__ __forceinline__ void load(const T* __restrict__ g, int64_t ld, int nvalid, int tid) {
+  uint32_t off[PER];
+  __device__ __forceinline__ void init(int64_t ld, int tid) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int u = tid + 256 * i;
-      r0[i] = make_uint4(0, 0, 0, 0);
+      int row, col;
       if constexpr (PAIR) {
-        r1[i] = make_uint4(0, 0, 0, 0);
-        const int kp = u % (ROWS / 2), col = (u / (ROWS / 2)) * EPV;
-        if (u < NU && 2 * kp < nvalid) r0[i] = *reinterpret_cast<const uint4*>(g + (2 * kp) * ld + col);
-        if (u < NU && 2 * kp + 1 < nvalid) r1[i] = *reinterpret_cast<const uint4*>(g + (2 * kp + 1) * ld + col);
+        row = 2 * (u % (ROWS / 2));
+        col = (u / (ROWS / 2)) * EPV;
       } else {
-        const int row = u % ROWS, col = (u / ROWS) * EPV;
-        if (u < NU && row < nvalid) r0[i] = *reinterpret_cast<const uint4*>(g + row * ld + col);
+        row = u % ROWS;
+        col = (u / ROWS) * EPV;
       }
+      off[i] = (uint32_t)(((int64_t)row * ld + col) * sizeof(T));
+    }
+  }
+  __device__ __forceinline__ void load(const T* __restrict__ g, int64_t ld, int nvalid, int tid) {
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(g, tile_bytes<T, D>(ld, min(nvalid, ROWS)));
+    const uint32_t step = (uint32_t)(ld * sizeof(T));
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      if (tid + 256 * i >= NU) continue;
+      r0[i] = buf_load16(rs, off[i]);
+      if constexpr (PAIR) r1[i] = buf_load16(rs, off[i] + step);
     }
   }
   __device__ __forceinline__ void store(T* __restrict__ lds, int tid) const {
@@ -249,14 +282,12 @@ struct TransTile {
       if (u >= NU) continue;
       if constexpr (PAIR) {
         const int kp = u % (ROWS / 2), col = (u / (ROWS / 2)) * EPV;
-        const uint32_t a[4] = {r0[i].x, r0[i].y, r0[i].z, r0[i].w};
-        const uint32_t b[4] = {r1[i].x, r1[i].y, r1[i].z, r1[i].w};
+        const uint32_t a4[4] = {r0[i].x, r0[i].y, r0[i].z, r0[i].w};
+        const uint32_t b4[4] = {r1[i].x, r1[i].y, r1[i].z, r1[i].w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          uint32_t lo = (a[e] & 0xffffu) | (b[e] << 16);
-          uint32_t hi = (a[e] >> 16) | (b[e] & 0xffff0000u);
-          *reinterpret_cast<uint32_t*>(lds + (col + 2 * e) * LDT + 2 * kp) = lo;
-          *reinterpret_cast<uint32_t*>(lds + (col + 2 * e + 1) * LDT + 2 * kp) = hi;
+          *reinterpret_cast<uint32_t*>(lds + (col + 2 * e) * LDT + 2 * kp) = __builtin_amdgcn_perm(b4[e], a4[e], 0x05040100u);
+          *reinterpret_cast<uint32_t*>(lds + (col + 2 * e + 1) * LDT + 2 * kp) = __builtin_amdgcn_perm(b4[e], a4[e], 0x07060302u);
         }
       } else {
         const int row = u % ROWS, col = (u / ROWS) * EPV;

@@ -8,7 +8,7 @@
  *
  * Tensors of shape [B, H, L, D] are described by fla_tensor4_t: a data pointer and
  * the element strides of the B, H and L dimensions; the D dimension must be
- * contiguous and rows must be 16-byte aligned.  dtype is one of FLA_F32, FLA_F16,
+ * contiguous, rows must be 16-byte aligned and 0 < stride_l * element size <= 16 MiB.  dtype is one of FLA_F32, FLA_F16,
  * FLA_BF16; D must be 32, 64 or 128 (callers pad smaller head dims with zeros and
  * pass the softmax scale of the true head dim).
  */
