@@ -127,6 +127,82 @@ def bench_entmax(dev, iters=200):
     }
 
 
+def rope(x, base=10000.0):
+    """Rotary position embedding (rotate-half convention) applied to [B, H, L, D]."""
+    B, H, L, D = x.shape
+    inv = 1.0 / (base ** (torch.arange(0, D, 2, device=x.device, dtype=torch.float32) / D))
+    ang = torch.arange(L, device=x.device, dtype=torch.float32)[:, None] * inv[None, :]
+    cos, sin = torch.cos(ang).repeat(1, 2), torch.sin(ang).repeat(1, 2)
+    xf = x.float()
+    x1, x2 = xf[..., : D // 2], xf[..., D // 2:]
+    rot = torch.cat((-x2, x1), dim=-1)
+    return (xf * cos + rot * sin).to(x.dtype)
+
+
+def bench_configs(dev, steps, warmup):
+    """The other BASELINE.json configs, each timed with HIP events on the launch stream."""
+    from adasplash import adasplash, adasplash_no_block_mask, lazy_attention_triton
+
+    res = {}
+    g = torch.Generator(device="cpu").manual_seed(0)
+
+    def rnd(*shape, scale=1.0):
+        return (torch.randn(*shape, generator=g) * scale).to(device=dev, dtype=torch.bfloat16)
+
+    # configs[1]: adasplash_no_block_mask forward, non-causal, [4, 12, 1024, 64]
+    q, k, v = rnd(4, 12, 1024, 64), rnd(4, 12, 1024, 64), rnd(4, 12, 1024, 64)
+    with torch.no_grad():
+        ms = time_region(lambda: adasplash_no_block_mask(q, k, v, alpha=1.5, niter=10, is_causal=False), steps, warmup)
+    res["cfg2_nomask_fwd_ms"] = ms
+    res["cfg2_nomask_fwd_TFLOPs"] = 4.0 * 4 * 12 * 1024 * 1024 * 64 / (ms * 1e-3) / 1e12
+
+    # configs[3]: varlen, 8 sequences with lengths U[512, 8192] padded to 8192, H=12
+    lens = torch.randint(512, 8193, (8,), generator=torch.Generator().manual_seed(0))
+    B, H, L, D = 8, 12, 8192, 64
+    q, k, v, do = (rnd(B, H, L, D) for _ in range(4))
+    qr, kr, vr = (t.clone().requires_grad_(True) for t in (q, k, v))
+    vl = lens.to(dev)
+    s2 = float((lens.double() ** 2).sum())
+    for causal in (True, False):
+        def run():
+            for t in (qr, kr, vr):
+                t.grad = None
+            adasplash(qr, kr, vr, alpha=1.5, niter=10, is_causal=causal, varlen=vl).backward(do)
+
+        ms = time_region(run, steps, warmup)
+        flops = (7.0 if causal else 14.0) * H * D * s2
+        tag = "causal" if causal else "bidir"
+        res[f"cfg4_varlen_{tag}_ms"] = ms
+        res[f"cfg4_varlen_{tag}_TFLOPs"] = flops / (ms * 1e-3) / 1e12
+    del q, k, v, do, qr, kr, vr
+
+    # configs[4]: lazy attention fwd+bwd, [2, 8, 4096, 64], RoPE pre-applied, bias [8, 512], tau = -1
+    B, H, L, D, W = 2, 8, 4096, 64, 512
+    q, k = rope(rnd(B, H, L, D)), rope(rnd(B, H, L, D))
+    v, do = rnd(B, H, L, D), rnd(B, H, L, D)
+    bias = (torch.randn(H, W, generator=g) * 0.02).to(dev).requires_grad_(True)
+    tau = torch.full((H,), -1.0, device=dev).requires_grad_(True)
+    qr, kr, vr = (t.clone().requires_grad_(True) for t in (q, k, v))
+
+    def run_lazy(varlen=None):
+        def r():
+            for t in (qr, kr, vr, bias, tau):
+                t.grad = None
+            lazy_attention_triton(qr, kr, vr, bias, tau, window_size=W, varlen=varlen).backward(do)
+
+        return r
+
+    ms = time_region(run_lazy(), steps, warmup)
+    res["cfg5_lazy_ms"] = ms
+    res["cfg5_lazy_TFLOPs"] = 7.0 * B * H * L * L * D / (ms * 1e-3) / 1e12  # causal fwd+bwd, FA convention
+    with torch.no_grad():
+        msf = time_region(lambda: lazy_attention_triton(q, k, v, bias, tau, window_size=W), steps, warmup)
+    res["cfg5_lazy_fwd_ms"] = msf
+    lvl = torch.randint(L // 8, L + 1, (B,), generator=torch.Generator().manual_seed(1)).to(dev)
+    res["cfg5_lazy_varlen_ms"] = time_region(run_lazy(lvl.to(torch.int32)), steps, warmup)
+    return res
+
+
 def cpu_baseline(shape, budget_s=12.0):
     """The CPU oracle (numpy float64 bisection entmax attention, forward + backward) on a
     bounded row sample of slice (b=0, h=0) at L=8192, extrapolated to the full step by the
@@ -202,7 +278,9 @@ def main():
     fwd, bwd = dense_flops(B, H, L, D)
     tflops = (fwd + bwd) / (res["ms_a15"] * 1e-3) / 1e12
     extra = dict(res)
-    extra.update(bench_entmax(dev) if not args.quick else {})
+    if not args.quick:
+        extra.update(bench_entmax(dev))
+        extra.update(bench_configs(dev, max(3, args.steps // 2), 2))
     extra["mfma_frac_fwd_bwd"] = tflops / PEAK_BF16_TFLOPS
     if "ms_a20" in res:
         extra["skip_speedup_a20"] = res["ms_a20_nomask"] / res["ms_a20"]
