@@ -30,6 +30,10 @@ import torch  # noqa: E402
 METRIC = "fwd+bwd ms & TFLOP/s (% MFMA peak) at L=8192 α=1.5 causal; entmax GB/s"
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBPS = 8000.0
+# HBM bytes per launch of ada_fwd_kernel at the headline config, from two rocprofv3 --pmc
+# passes (FETCH_SIZE x2.000, WRITE_SIZE x1.000 after calibration on a plain 256 MiB copy);
+# source: profiles/adasplash_causal_L8192_a15_traffic.txt.
+FWD_TRAFFIC_BYTES = (131181 * 2.0 + 99397 * 1.0) * 1024
 
 
 def dense_flops(B, H, L, D, causal=True):
@@ -265,7 +269,17 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline step only (for profiling runs)")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="only copy a 256 MiB buffer 3 times (calibrates the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
+    if args.calib_copy:
+        src = torch.ones(64 << 20, device="cuda")  # 256 MiB
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calib_copy_bytes": src.numel() * 4}))
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: every op shards over (B, H) with no communication, "
               "so multi-GPU runs are out of scope for this build.", file=sys.stderr)
@@ -309,7 +323,7 @@ def main():
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": FWD_TRAFFIC_BYTES,
         },
         "extra": {k_: (round(v_, 4) if isinstance(v_, float) else v_) for k_, v_ in extra.items()},
     }
