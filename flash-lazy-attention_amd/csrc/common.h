@@ -347,6 +347,16 @@ __device__ __forceinline__ void store_acc_row(typename Tr<DT>::T* rowp, const f3
 // LDS available to one workgroup on gfx950, and the waves-per-SIMD target of the main
 // kernels (16-bit inputs fit two workgroups per CU; fp32 tiles need the whole register file).
 static constexpr int LDS_LIMIT = 160 * 1024;
+
+// Row padding (elements) of LDS tiles stored transposed ([D][64]) and read back with
+// load_perm_frag.  Those reads are 8 bytes per lane for 16-bit types (4 bytes for fp32) from
+// 32 consecutive rows; a row stride of 34 (resp. 65) dwords puts the rows of one read on
+// distinct banks, where the 16-byte padding of the row-major tiles (36 dwords) would
+// make rows r and r+8 collide.
+template <typename T>
+struct TransPad {
+  static constexpr int value = sizeof(T) == 2 ? 4 : 1;
+};
 template <int DT>
 struct Occ {
   static constexpr int value = DT == F32 ? 1 : 2;
