@@ -184,8 +184,23 @@ __device__ __forceinline__ void stage_rows_t(T* __restrict__ lds, const T* __res
   }
 }
 
-// t = (alpha-1)*scale*s - tau as one fused multiply-add.  Every kernel that decides
-// p > 0 uses this same expression, so they agree on the support for the same score.
+// max(x, 0) as an integer max on the bit pattern (every negative float, -0 and -inf included,
+// has a negative pattern).  One v_max_i32, where fmaxf on an MFMA result would first
+// canonicalise its operand.  x must not be NaN.
+__device__ __forceinline__ float pos_part(float x) { return __int_as_float(max(__float_as_int(x), 0)); }
+// Whether any of the 32 values is > 0 (same bit-pattern argument: positive floats are exactly
+// the positive patterns).
+__device__ __forceinline__ bool any_pos(const f32x16& a, const f32x16& b) {
+  int m = 0;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) m = max(m, max(__float_as_int(a[r]), __float_as_int(b[r])));
+  return m > 0;
+}
+
+// t = (alpha-1)*scale*s - tau as one fused multiply-add (threshold search over stored scores).
+// The sweeps that produce p for the output and the gradients (forward pass B, both backward
+// kernels) instead start the q.k MFMA from -tau/cz, all with the same fp32 value, so they agree
+// with each other on the support and the block mask.
 __device__ __forceinline__ float zt(float s, float cz, float tau) { return __builtin_fmaf(s, cz, -tau); }
 
 // Buffer resource over [base, base + bytes): raw buffer loads past the end return zero, which
