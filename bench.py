@@ -95,13 +95,13 @@ def bench_attention(args, dev):
     def fwd_call():
         rc = L_.lib().fla_adasplash_fwd(
             L_.t4(qp), L_.t4(kp), L_.t4(vp), L_.t4(out), L_.ptr(tau), L_.ptr(wn), L_.ptr(mask), None,
-            B, H, L, D, L_.FLA_BF16, 1.5, 10, 1, 1, scale, L_.stream_of(q))
+            B, H, H, L, D, L_.FLA_BF16, 1.5, 10, 1, 1, scale, L_.stream_of(q))
         L_.check(rc, "fwd")
 
     def bwd_call():
         rc = L_.lib().fla_adasplash_bwd(
             L_.t4(qp), L_.t4(kp), L_.t4(vp), L_.t4(do), L_.t4(dq), L_.t4(dk), L_.t4(dv), L_.ptr(tau), L_.ptr(wn),
-            L_.ptr(mask), None, L_.ptr(delta), B, H, L, D, L_.FLA_BF16, 1.5, 1, scale, L_.stream_of(q))
+            L_.ptr(mask), None, L_.ptr(delta), B, H, H, L, D, L_.FLA_BF16, 1.5, 1, scale, L_.stream_of(q))
         L_.check(rc, "bwd")
 
     res["fwd_kernel_ms"] = time_region(fwd_call, args.steps, args.warmup)

@@ -39,18 +39,18 @@ SIGNATURES = {
     "fla_entmax_bwd": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _F, _P], _I),
     "fla_adasplash_mask_words": ([_I], _I),
     "fla_adasplash_fwd": (
-        [_T4, _T4, _T4, _T4, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _I, _I, _F, _P],
+        [_T4, _T4, _T4, _T4, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I, _I, _I, _F, _P],
         _I,
     ),
     "fla_adasplash_bwd": (
-        [_T4, _T4, _T4, _T4, _T4, _T4, _T4, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _F, _P],
+        [_T4, _T4, _T4, _T4, _T4, _T4, _T4, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I, _F, _P],
         _I,
     ),
-    "fla_lazy_fwd": ([_T4, _T4, _T4, _T4, _P, _I64, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P], _I),
+    "fla_lazy_fwd": ([_T4, _T4, _T4, _T4, _P, _I64, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P], _I),
     "fla_lazy_bwd_workspace_size": ([_I, _I, _I, _I], ctypes.c_size_t),
     "fla_lazy_bwd": (
         [_T4, _T4, _T4, _T4, _T4, _T4, _T4, _P, _I64, _P, _I, _P, _P, _P, _P, _P, _P, ctypes.c_size_t,
-         _I, _I, _I, _I, _I, _F, _P],
+         _I, _I, _I, _I, _I, _I, _F, _P],
         _I,
     ),
 }
@@ -129,9 +129,13 @@ def check_inputs(q, k, v):
         raise TypeError(f"unsupported dtype {q.dtype}; expected float32, float16 or bfloat16")
     if k.dtype != q.dtype or v.dtype != q.dtype:
         raise TypeError("q, k, v must share one dtype")
-    if q.shape != k.shape or q.shape != v.shape:
-        raise ValueError(f"q, k, v shapes differ: {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
-    return q.shape[-1], 1.0 / math.sqrt(q.shape[-1])
+    if q.dim() != 4 or k.shape != v.shape or k.dim() != 4:
+        raise ValueError(f"expected [B, H, L, D] q and matching k, v; got {tuple(q.shape)}, {tuple(k.shape)}, "
+                         f"{tuple(v.shape)}")
+    B, H, L, D = q.shape
+    if k.shape[0] != B or k.shape[2] != L or k.shape[3] != D or k.shape[1] <= 0 or H % k.shape[1]:
+        raise ValueError(f"k, v must be [B, H_kv, L, D] with H_kv dividing H={H}; got {tuple(k.shape)}")
+    return D, 1.0 / math.sqrt(D)
 
 
 def prep_varlen(varlen, B, device):

@@ -5,7 +5,9 @@ varlen=None)`` (block-masked) and ``adasplash.adasplash_no_block_mask(...)``
 (reference README.md:39-58; behaviour pinned by tests/test_adasplash.py and
 tests/test_adasplash_no_block_mask.py).
 
-q, k, v: [B, H, L, D] float32 / float16 / bfloat16 on the GPU, D <= 128.
+q: [B, H, L, D], k, v: [B, H_kv, L, D] with H_kv dividing H (grouped-query attention: query
+head h attends to K/V head h // (H / H_kv), read in place); float32 / float16 / bfloat16 on the
+GPU, D <= 128.
 varlen: optional [B] true lengths; keys j >= varlen[b] are masked and output rows
 i >= varlen[b] are exactly zero.  The softmax scale is 1/sqrt(D).
 The block-masked variant also records which (128-query x 64-key) tiles hold any p > 0
@@ -45,7 +47,7 @@ def _forward(q, k, v, alpha, niter, is_causal, varlen, use_mask, need_grad_state
         mask = torch.empty((B, H, (L + 127) // 128, mw), device=q.device, dtype=torch.int32)
     rc = lib().fla_adasplash_fwd(
         t4(qp), t4(kp), t4(vp), t4(out), ptr(tau), ptr(wn), ptr(mask), ptr(vl),
-        B, H, L, Dk, DTYPE_CODE[q.dtype], alpha, int(niter), int(bool(is_causal)), int(bool(use_mask)), scale,
+        B, H, kp.shape[1], L, Dk, DTYPE_CODE[q.dtype], alpha, int(niter), int(bool(is_causal)), int(bool(use_mask)), scale,
         stream_of(q),
     )
     check(rc, "fla_adasplash_fwd")
@@ -74,7 +76,7 @@ class AdaSplashFunction(torch.autograd.Function):
         delta = torch.empty((B, H, L), device=qp.device, dtype=torch.float32)
         rc = lib().fla_adasplash_bwd(
             t4(qp), t4(kp), t4(vp), t4(dop), t4(dq), t4(dk), t4(dv), ptr(tau), ptr(wn), ptr(mask), ptr(vl),
-            ptr(delta), B, H, L, Dk, DTYPE_CODE[qp.dtype], alpha, int(is_causal), scale, stream_of(qp),
+            ptr(delta), B, H, kp.shape[1], L, Dk, DTYPE_CODE[qp.dtype], alpha, int(is_causal), scale, stream_of(qp),
         )
         check(rc, "fla_adasplash_bwd")
         if Dk != D:

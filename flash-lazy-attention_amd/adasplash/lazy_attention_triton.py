@@ -5,7 +5,9 @@ and ``LazyAttentionTritonFunc`` (reference lazy_attention_triton.py:503-541):
 
     out_i = sum_{j <= i} relu(softmax_j(q_i.k_j/sqrt(D) + bias[h, i-j]*1[0 <= i-j < W]) + tau_h/(i+1)) v_j
 
-q, k, v: [B, H, L, D] (RoPE already applied), bias [H, >= W], tau [H], varlen optional [B].
+q: [B, H, L, D], k, v: [B, H_kv, L, D] (RoPE already applied; H_kv dividing H, query head h
+reading K/V head h // (H / H_kv) in place, with no repeat_interleave), bias [H, >= W], tau [H],
+varlen optional [B].
 Gradients: dq, dk, dv in the input dtype; dbias / dtau in float32 and only when bias / tau
 require grad (lazy_attention_triton.py:523-539).  Rows i >= varlen[b] are zero in the output
 and in every gradient.
@@ -51,7 +53,7 @@ def _forward(q, k, v, bias, tau, window_size, varlen, need_w):
     wd = torch.empty((B, H, L, Dk), device=q.device, dtype=torch.float32) if need_w else None
     rc = lib().fla_lazy_fwd(
         t4(qp), t4(kp), t4(vp), t4(out), ptr(b32), b32.shape[1], ptr(t32), W, ptr(lse), ptr(wd), ptr(vl),
-        B, H, L, Dk, DTYPE_CODE[q.dtype], scale, stream_of(q),
+        B, H, kp.shape[1], L, Dk, DTYPE_CODE[q.dtype], scale, stream_of(q),
     )
     check(rc, "fla_lazy_fwd")
     return out, lse, wd, (qp, kp, vp), b32, t32, W, vl, D, Dk, scale
@@ -84,7 +86,7 @@ class LazyAttentionTritonFunc(torch.autograd.Function):
         ws = torch.empty((nbytes,), device=qp.device, dtype=torch.uint8)
         rc = lib().fla_lazy_bwd(
             t4(qp), t4(kp), t4(vp), t4(dop), t4(dq), t4(dk), t4(dv), ptr(b32), b32.shape[1], ptr(t32), W,
-            ptr(lse), ptr(wd), ptr(vl), ptr(dbias), ptr(dtau), ptr(ws), nbytes, B, H, L, Dk,
+            ptr(lse), ptr(wd), ptr(vl), ptr(dbias), ptr(dtau), ptr(ws), nbytes, B, H, kp.shape[1], L, Dk,
             DTYPE_CODE[qp.dtype], scale, stream_of(qp),
         )
         check(rc, "fla_lazy_bwd")

@@ -64,9 +64,10 @@ extern "C" int fla_adasplash_mask_words(int L) {
 
 extern "C" int fla_adasplash_fwd(const fla_tensor4_t* q, const fla_tensor4_t* k, const fla_tensor4_t* v,
                                  const fla_tensor4_t* out, float* tau, float* wn, uint32_t* block_mask,
-                                 const int32_t* varlen, int B, int H, int L, int D, int dtype, float alpha, int niter,
+                                 const int32_t* varlen, int B, int H, int Hkv, int L, int D, int dtype, float alpha, int niter,
                                  int is_causal, int skip_empty_blocks, float scale, void* stream) {
   if (!good_common(B, H, L, D, dtype)) return FLA_EINVAL;
+  if (Hkv <= 0 || H % Hkv) return FLA_EINVAL;
   if (!good_tensor(q, dtype) || !good_tensor(k, dtype) || !good_tensor(v, dtype) || !good_tensor(out, dtype))
     return FLA_EINVAL;
   if (!tau || !(alpha > 1.0f) || alpha > 2.0f || !(scale > 0.0f)) return FLA_EINVAL;
@@ -81,6 +82,7 @@ extern "C" int fla_adasplash_fwd(const fla_tensor4_t* q, const fla_tensor4_t* k,
   a.varlen = varlen;
   a.B = B;
   a.H = H;
+  a.G = H / Hkv;
   a.L = L;
   a.Tr = (L + 127) / 128;
   a.MW = fla_adasplash_mask_words(L);
@@ -99,9 +101,10 @@ extern "C" int fla_adasplash_fwd(const fla_tensor4_t* q, const fla_tensor4_t* k,
 extern "C" int fla_adasplash_bwd(const fla_tensor4_t* q, const fla_tensor4_t* k, const fla_tensor4_t* v,
                                  const fla_tensor4_t* dout, const fla_tensor4_t* dq, const fla_tensor4_t* dk,
                                  const fla_tensor4_t* dv, const float* tau, const float* wn,
-                                 const uint32_t* block_mask, const int32_t* varlen, float* delta_ws, int B, int H,
+                                 const uint32_t* block_mask, const int32_t* varlen, float* delta_ws, int B, int H, int Hkv,
                                  int L, int D, int dtype, float alpha, int is_causal, float scale, void* stream) {
   if (!good_common(B, H, L, D, dtype)) return FLA_EINVAL;
+  if (Hkv <= 0 || H % Hkv) return FLA_EINVAL;
   if (!good_tensor(q, dtype) || !good_tensor(k, dtype) || !good_tensor(v, dtype) || !good_tensor(dout, dtype) ||
       !good_tensor(dq, dtype) || !good_tensor(dk, dtype) || !good_tensor(dv, dtype))
     return FLA_EINVAL;
@@ -121,6 +124,7 @@ extern "C" int fla_adasplash_bwd(const fla_tensor4_t* q, const fla_tensor4_t* k,
   a.delta = delta_ws;
   a.B = B;
   a.H = H;
+  a.G = H / Hkv;
   a.L = L;
   a.Tr = (L + 127) / 128;
   a.MW = fla_adasplash_mask_words(L);
@@ -146,9 +150,10 @@ extern "C" size_t fla_lazy_bwd_workspace_size(int B, int H, int L, int window) {
 
 extern "C" int fla_lazy_fwd(const fla_tensor4_t* q, const fla_tensor4_t* k, const fla_tensor4_t* v,
                             const fla_tensor4_t* out, const float* bias, int64_t bias_ld, const float* tau,
-                            int window, float* lse, float* wdelta, const int32_t* varlen, int B, int H, int L, int D,
+                            int window, float* lse, float* wdelta, const int32_t* varlen, int B, int H, int Hkv, int L, int D,
                             int dtype, float scale, void* stream) {
   if (!good_common(B, H, L, D, dtype)) return FLA_EINVAL;
+  if (Hkv <= 0 || H % Hkv) return FLA_EINVAL;
   if (!good_tensor(q, dtype) || !good_tensor(k, dtype) || !good_tensor(v, dtype) || !good_tensor(out, dtype))
     return FLA_EINVAL;
   if (!bias || !tau || !lse || window <= 0 || bias_ld < window || !(scale > 0.0f)) return FLA_EINVAL;
@@ -165,6 +170,7 @@ extern "C" int fla_lazy_fwd(const fla_tensor4_t* q, const fla_tensor4_t* k, cons
   a.varlen = varlen;
   a.B = B;
   a.H = H;
+  a.G = H / Hkv;
   a.L = L;
   a.W = window;
   a.nQT = (L + 127) / 128;
@@ -179,9 +185,10 @@ extern "C" int fla_lazy_bwd(const fla_tensor4_t* q, const fla_tensor4_t* k, cons
                             const fla_tensor4_t* dout, const fla_tensor4_t* dq, const fla_tensor4_t* dk,
                             const fla_tensor4_t* dv, const float* bias, int64_t bias_ld, const float* tau, int window,
                             const float* lse, const float* wdelta, const int32_t* varlen, float* dbias, float* dtau,
-                            void* workspace, size_t workspace_bytes, int B, int H, int L, int D, int dtype,
+                            void* workspace, size_t workspace_bytes, int B, int H, int Hkv, int L, int D, int dtype,
                             float scale, void* stream) {
   if (!good_common(B, H, L, D, dtype)) return FLA_EINVAL;
+  if (Hkv <= 0 || H % Hkv) return FLA_EINVAL;
   if (!good_tensor(q, dtype) || !good_tensor(k, dtype) || !good_tensor(v, dtype) || !good_tensor(dout, dtype) ||
       !good_tensor(dq, dtype) || !good_tensor(dk, dtype) || !good_tensor(dv, dtype))
     return FLA_EINVAL;
@@ -205,6 +212,7 @@ extern "C" int fla_lazy_bwd(const fla_tensor4_t* q, const fla_tensor4_t* k, cons
   a.varlen = varlen;
   a.B = B;
   a.H = H;
+  a.G = H / Hkv;
   a.L = L;
   a.W = window;
   a.nQT = (L + 127) / 128;

@@ -12,6 +12,7 @@ struct AdaFwdArgs {
   uint32_t* mask;          // [B, H, Tr, MW] block mask, optional
   const int32_t* varlen;   // [B], optional
   int B, H, L, Tr, MW;
+  int G;                   // query heads per K/V head (K/V have H / G heads)
   float cz, beta;          // cz = (alpha-1)*scale, beta = 1/(alpha-1)
   int causal, skip, fb_maxit;
 };
@@ -24,6 +25,7 @@ struct AdaBwdArgs {
   const int32_t* varlen;
   float* delta;            // [B, H, L] scratch
   int B, H, L, Tr, MW;
+  int G;                   // query heads per K/V head
   float cz, beta, scale;
   int causal;
 };
@@ -42,6 +44,7 @@ struct LazyArgs {
   float* dbias;            // [H, window]
   float* dtau;             // [H]
   int B, H, L, W, nQT;
+  int G;                   // query heads per K/V head
   float scale;
 };
 

@@ -11,6 +11,11 @@
  * contiguous, rows must be 16-byte aligned and 0 < stride_l * element size <= 16 MiB.  dtype is one of FLA_F32, FLA_F16,
  * FLA_BF16; D must be 32, 64 or 128 (callers pad smaller head dims with zeros and
  * pass the softmax scale of the true head dim).
+ *
+ * Attention entry points take H query heads and Hkv key/value heads (H % Hkv == 0):
+ * query head h reads K/V head h / (H / Hkv) in place (grouped-query attention without a
+ * repeat_interleave copy); k, v, dk, dv have Hkv heads, everything per row has H.  Hkv = H
+ * is ordinary multi-head attention.
  */
 #ifndef FLASHLAZY_H
 #define FLASHLAZY_H
@@ -70,7 +75,7 @@ int fla_adasplash_mask_words(int L);
  * convergence (niter raises the cap of the full-sweep fallback). */
 int fla_adasplash_fwd(const fla_tensor4_t* q, const fla_tensor4_t* k, const fla_tensor4_t* v,
                       const fla_tensor4_t* out, float* tau, float* wn, uint32_t* block_mask, const int32_t* varlen,
-                      int B, int H, int L, int D, int dtype, float alpha, int niter, int is_causal,
+                      int B, int H, int Hkv, int L, int D, int dtype, float alpha, int niter, int is_causal,
                       int skip_empty_blocks, float scale, void* stream);
 
 /* AdaSplash backward (dq, dk, dv) through the entmax Jacobian, from the forward's
@@ -79,7 +84,7 @@ int fla_adasplash_fwd(const fla_tensor4_t* q, const fla_tensor4_t* k, const fla_
 int fla_adasplash_bwd(const fla_tensor4_t* q, const fla_tensor4_t* k, const fla_tensor4_t* v,
                       const fla_tensor4_t* dout, const fla_tensor4_t* dq, const fla_tensor4_t* dk,
                       const fla_tensor4_t* dv, const float* tau, const float* wn, const uint32_t* block_mask,
-                      const int32_t* varlen, float* delta_ws, int B, int H, int L, int D, int dtype, float alpha,
+                      const int32_t* varlen, float* delta_ws, int B, int H, int Hkv, int L, int D, int dtype, float alpha,
                       int is_causal, float scale, void* stream);
 
 /* Lazy attention forward: causal elastic softmax relu(softmax(q k^T*scale + bias) + tau_h/(i+1)) v
@@ -92,7 +97,7 @@ int fla_adasplash_bwd(const fla_tensor4_t* q, const fla_tensor4_t* k, const fla_
  *   varlen [B] int32, optional. */
 int fla_lazy_fwd(const fla_tensor4_t* q, const fla_tensor4_t* k, const fla_tensor4_t* v, const fla_tensor4_t* out,
                  const float* bias, int64_t bias_ld, const float* tau, int window, float* lse, float* wdelta,
-                 const int32_t* varlen, int B, int H, int L, int D, int dtype, float scale, void* stream);
+                 const int32_t* varlen, int B, int H, int Hkv, int L, int D, int dtype, float scale, void* stream);
 
 /* Bytes of caller-provided scratch that fla_lazy_bwd needs (per-tile dbias / dtau partials). */
 size_t fla_lazy_bwd_workspace_size(int B, int H, int L, int window);
@@ -104,7 +109,7 @@ int fla_lazy_bwd(const fla_tensor4_t* q, const fla_tensor4_t* k, const fla_tenso
                  const fla_tensor4_t* dq, const fla_tensor4_t* dk, const fla_tensor4_t* dv, const float* bias,
                  int64_t bias_ld, const float* tau, int window, const float* lse, const float* wdelta,
                  const int32_t* varlen, float* dbias, float* dtau, void* workspace, size_t workspace_bytes, int B,
-                 int H, int L, int D, int dtype, float scale, void* stream);
+                 int H, int Hkv, int L, int D, int dtype, float scale, void* stream);
 
 #ifdef __cplusplus
 }

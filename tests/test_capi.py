@@ -56,23 +56,26 @@ def test_argument_validation_without_gpu():
     t = L.Tensor4(base, 64 * 64, 64 * 64, 64)
     tp = ctypes.byref(t)
     # head dim 48 is not a kernel head dim
-    assert lib.fla_adasplash_fwd(tp, tp, tp, tp, base, None, None, None, 1, 1, 64, 48, L.FLA_BF16, 1.5, 10, 0, 1,
+    assert lib.fla_adasplash_fwd(tp, tp, tp, tp, base, None, None, None, 1, 1, 1, 64, 48, L.FLA_BF16, 1.5, 10, 0, 1,
                                  0.125, None) == -1
     # alpha outside (1, 2]
-    assert lib.fla_adasplash_fwd(tp, tp, tp, tp, base, None, None, None, 1, 1, 64, 64, L.FLA_BF16, 2.5, 10, 0, 1,
+    assert lib.fla_adasplash_fwd(tp, tp, tp, tp, base, None, None, None, 1, 1, 1, 64, 64, L.FLA_BF16, 2.5, 10, 0, 1,
                                  0.125, None) == -1
     # misaligned row stride
     bad = L.Tensor4(base, 64 * 64, 64 * 64, 63)
-    assert lib.fla_adasplash_fwd(ctypes.byref(bad), tp, tp, tp, base, None, None, None, 1, 1, 64, 64, L.FLA_BF16,
+    assert lib.fla_adasplash_fwd(ctypes.byref(bad), tp, tp, tp, base, None, None, None, 1, 1, 1, 64, 64, L.FLA_BF16,
                                  1.5, 10, 0, 1, 0.125, None) == -1
     # unknown dtype
     assert lib.fla_entmax_fwd(base, base, 4, 8, 8, 8, 7, 1.5, 10, 1, None) == -1
     # lazy backward without workspace
     assert lib.fla_lazy_bwd(tp, tp, tp, tp, tp, tp, tp, base, 64, base, 16, base, base, None, None, None, None, 0, 1,
-                            1, 64, 64, L.FLA_BF16, 0.125, None) == -3
+                            1, 1, 64, 64, L.FLA_BF16, 0.125, None) == -3
     # dbias without dtau
     assert lib.fla_lazy_bwd(tp, tp, tp, tp, tp, tp, tp, base, 64, base, 16, base, base, None, base, None, None, 0, 1,
-                            1, 64, 64, L.FLA_BF16, 0.125, None) == -1
+                            1, 1, 64, 64, L.FLA_BF16, 0.125, None) == -1
+    # H not a multiple of H_kv
+    assert lib.fla_adasplash_fwd(tp, tp, tp, tp, base, None, None, None, 1, 3, 2, 64, 64, L.FLA_BF16, 1.5, 10, 0, 1,
+                                 0.125, None) == -1
 
 
 def test_host_layout_helpers():
