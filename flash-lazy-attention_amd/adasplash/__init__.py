@@ -1,10 +1,12 @@
 """AdaSplash / Lazy attention for AMD Instinct MI355X (gfx950), hand-written HIP kernels.
 
 Drop-in names of the reference package (README.md:25-137):
-``triton_entmax``, ``adasplash``, ``adasplash_no_block_mask``, ``lazy_attention_triton``.
+``triton_entmax``, ``adasplash``, ``adasplash_no_block_mask``, ``lazy_attention_triton``,
+and the ``LazyAttention`` layer (``adasplash.lazy_attention``, tests/test_lazy_attention.py).
 """
 from .adasplash_block_mask import adasplash, adasplash_stats
 from .adasplash_no_block_mask import adasplash_no_block_mask
+from .lazy_attention import LazyAttention, RotaryEmbedding
 from .lazy_attention_triton import LazyAttentionTritonFunc, lazy_attention_triton
 from .triton_entmax import triton_entmax
 
@@ -15,4 +17,6 @@ __all__ = [
     "adasplash_stats",
     "lazy_attention_triton",
     "LazyAttentionTritonFunc",
+    "LazyAttention",
+    "RotaryEmbedding",
 ]

@@ -98,6 +98,28 @@ def test_varlen_backward(tauval):
         assert (t.grad[0, :, 32:] == 0).all() and (t.grad[1, :, 48:] == 0).all()
 
 
+@pytest.mark.parametrize("varlen", [[90, 200], [64, 130]])
+def test_varlen_whole_row_tiles_past_length(varlen):
+    # Row tiles of 128 queries that start at or past varlen[b] while the window-free key range
+    # before them is non-empty: they must do no work and write exact zeros (regression: they
+    # once swept key tiles that were never loaded).
+    banner("lazy varlen empty row tiles", varlen)
+    B, H, L, D, W = 2, 2, 260, 32, 40
+    q, k, v, bias, tau = _case(B, H, L, D, W, torch.float32, seed=8, tau=0.2)
+    do = rand((B, H, L, D), torch.float32, 9)
+    ref = lazy_forward(to_np(q), to_np(k), to_np(v), to_np(bias), to_np(tau), W, np.array(varlen))
+    rg = lazy_backward(to_np(q), to_np(k), to_np(v), to_np(bias), to_np(tau), to_np(do), W, np.array(varlen))
+    ts = [t.to(DEV).requires_grad_(True) for t in (q, k, v, bias, tau)]
+    for _rep in range(3):
+        for t in ts:
+            t.grad = None
+        out = _op()(*ts, window_size=W, varlen=torch.tensor(varlen, dtype=torch.int32, device=DEV))
+        assert_close(to_np(out), ref, 1e-5, "forward")
+        out.backward(do.to(DEV))
+        for got, r, n in zip([t.grad for t in ts], rg, ["dq", "dk", "dv", "dbias", "dtau"]):
+            assert_close(to_np(got), r, 1e-4 * max(1.0, np.abs(r).max()), n)
+
+
 def test_frozen_parameters_fast_path():
     q, k, v, bias, tau = _case(1, 2, 96, 64, 16, torch.float32, seed=4)
     do = rand((1, 2, 96, 64), torch.float32, 5)
