@@ -46,7 +46,7 @@ SIGNATURES = {
         [_T4, _T4, _T4, _T4, _T4, _T4, _T4, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I, _F, _P],
         _I,
     ),
-    "fla_lazy_fwd": ([_T4, _T4, _T4, _T4, _P, _I64, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P], _I),
+    "fla_lazy_fwd": ([_T4, _T4, _T4, _T4, _P, _I64, _P, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I, _F, _P], _I),
     "fla_lazy_bwd_workspace_size": ([_I, _I, _I, _I], ctypes.c_size_t),
     "fla_lazy_bwd": (
         [_T4, _T4, _T4, _T4, _T4, _T4, _T4, _P, _I64, _P, _I, _P, _P, _P, _P, _P, _P, ctypes.c_size_t,
@@ -145,3 +145,10 @@ def prep_varlen(varlen, B, device):
     if vl.numel() != B:
         raise ValueError(f"varlen must have B={B} entries, got {vl.numel()}")
     return vl.to(torch.int32).contiguous()
+
+
+def unpack_block_mask(words, ncols):
+    """int32 [..., R, MW] bit rows (bit c%32 of word c/32 = column c) -> bool [..., R, ncols]."""
+    bits = torch.arange(32, device=words.device, dtype=torch.int32)
+    m = (words.unsqueeze(-1) >> bits) & 1
+    return m.reshape(*words.shape[:-1], -1)[..., :ncols].bool()

@@ -11,6 +11,11 @@ varlen optional [B].
 Gradients: dq, dk, dv in the input dtype; dbias / dtau in float32 and only when bias / tau
 require grad (lazy_attention_triton.py:523-539).  Rows i >= varlen[b] are zero in the output
 and in every gradient.
+
+``return_mask=True`` (the block sparsity planned at CURSOR_TASKS.md:214-312) also returns
+``bmask`` bool [B, H, ceil(L/64), ceil(L/64)]: block (r, c) is True iff some weight
+relu(p + tau/i) > 0 links a query of rows 64r.. to a key of 64c..; the forward then skips the
+P V products of empty tiles.  ``get_sparsity_stats(bmask)`` summarises it.
 """
 import torch
 
@@ -25,6 +30,7 @@ from ._lib import (
     ptr,
     stream_of,
     t4,
+    unpack_block_mask,
 )
 
 
@@ -41,7 +47,7 @@ def _params(bias, tau, H, window_size):
     return b32, t32, W
 
 
-def _forward(q, k, v, bias, tau, window_size, varlen, need_w):
+def _forward(q, k, v, bias, tau, window_size, varlen, need_w, want_mask=False):
     D, scale = check_inputs(q, k, v)
     Dk = kernel_head_dim(D)
     qp, kp, vp = (prep_bhld(x, Dk) for x in (q, k, v))
@@ -51,27 +57,37 @@ def _forward(q, k, v, bias, tau, window_size, varlen, need_w):
     out = torch.empty((B, H, L, Dk), device=q.device, dtype=q.dtype)
     lse = torch.empty((B, H, L), device=q.device, dtype=torch.float32)
     wd = torch.empty((B, H, L, Dk), device=q.device, dtype=torch.float32) if need_w else None
+    mask = None
+    if want_mask:
+        mw = lib().fla_adasplash_mask_words(L)
+        mask = torch.empty((B, H, (L + 63) // 64, mw), device=q.device, dtype=torch.int32)
     rc = lib().fla_lazy_fwd(
-        t4(qp), t4(kp), t4(vp), t4(out), ptr(b32), b32.shape[1], ptr(t32), W, ptr(lse), ptr(wd), ptr(vl),
+        t4(qp), t4(kp), t4(vp), t4(out), ptr(b32), b32.shape[1], ptr(t32), W, ptr(lse), ptr(wd),
+        ptr(mask), int(want_mask), ptr(vl),
         B, H, kp.shape[1], L, Dk, DTYPE_CODE[q.dtype], scale, stream_of(q),
     )
     check(rc, "fla_lazy_fwd")
-    return out, lse, wd, (qp, kp, vp), b32, t32, W, vl, D, Dk, scale
+    bmask = unpack_block_mask(mask, (L + 63) // 64) if want_mask else None
+    return out, lse, wd, (qp, kp, vp), b32, t32, W, vl, D, Dk, scale, bmask
 
 
 class LazyAttentionTritonFunc(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, q, k, v, bias, tau, window_size, varlen=None):
-        out, lse, wd, (qp, kp, vp), b32, t32, W, vl, D, Dk, scale = _forward(
-            q, k, v, bias, tau, window_size, varlen, True
+    def forward(ctx, q, k, v, bias, tau, window_size, varlen=None, want_mask=False):
+        out, lse, wd, (qp, kp, vp), b32, t32, W, vl, D, Dk, scale, bmask = _forward(
+            q, k, v, bias, tau, window_size, varlen, True, want_mask
         )
         ctx.save_for_backward(qp, kp, vp, b32, t32, lse, wd, vl)
         ctx.cfg = (W, D, Dk, scale, tuple(bias.shape))
         ctx.tau_shape = tuple(tau.shape)
-        return out[..., :D] if Dk != D else out
+        out = out[..., :D] if Dk != D else out
+        if want_mask:
+            ctx.mark_non_differentiable(bmask)
+            return out, bmask
+        return out
 
     @staticmethod
-    def backward(ctx, do):
+    def backward(ctx, do, *_dmask):
         qp, kp, vp, b32, t32, lse, wd, vl = ctx.saved_tensors
         W, D, Dk, scale, bshape = ctx.cfg
         B, H, L, _ = qp.shape
@@ -98,14 +114,31 @@ class LazyAttentionTritonFunc(torch.autograd.Function):
             dbias = full
         if need:
             dtau = dtau.reshape(ctx.tau_shape)
-        return dq, dk, dv, dbias, dtau, None, None
+        return dq, dk, dv, dbias, dtau, None, None, None
 
 
-def lazy_attention_triton(q, k, v, bias, tau, window_size=None, varlen=None):
+def lazy_attention_triton(q, k, v, bias, tau, window_size=None, varlen=None, return_mask=False):
     if window_size is None:
         window_size = bias.shape[1]
     if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v, bias, tau)):
-        return LazyAttentionTritonFunc.apply(q, k, v, bias, tau, window_size, varlen)
-    out, *_rest = _forward(q, k, v, bias, tau, window_size, varlen, False)
+        return LazyAttentionTritonFunc.apply(q, k, v, bias, tau, window_size, varlen, bool(return_mask))
+    res = _forward(q, k, v, bias, tau, window_size, varlen, False, bool(return_mask))
+    out, bmask = res[0], res[-1]
     D = q.shape[-1]
-    return out[..., :D] if out.shape[-1] != D else out
+    out = out[..., :D] if out.shape[-1] != D else out
+    return (out, bmask) if return_mask else out
+
+
+def get_sparsity_stats(bmask):
+    """Block statistics of a ``return_mask`` mask (CURSOR_TASKS.md:246-258): ``block_density``
+    (fraction of all blocks that are non-empty), ``visible_density`` (fraction of the causally
+    visible blocks c <= r that are non-empty) and ``theoretical_speedup`` = 1 / block_density."""
+    R, C = bmask.shape[-2:]
+    vis = torch.ones(R, C, dtype=torch.bool, device=bmask.device).tril()
+    density = bmask.float().mean().item()
+    nvis = vis.sum().item() * (bmask.numel() // (R * C))
+    return {
+        "block_density": density,
+        "visible_density": (bmask & vis).sum().item() / max(nvis, 1),
+        "theoretical_speedup": 1.0 / max(density, 0.01),
+    }

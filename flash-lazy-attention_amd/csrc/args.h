@@ -43,6 +43,9 @@ struct LazyArgs {
   float* dtau_part;        // [B*H*nQT]
   float* dbias;            // [H, window]
   float* dtau;             // [H]
+  uint32_t* mask;          // [B, H, ceil(L/64), MW] bits of (64-row, 64-key) blocks with e > 0, optional
+  int skip;                // skip the P V products of all-zero (wave, tile) pairs
+  int MW;
   int B, H, L, W, nQT;
   int G;                   // query heads per K/V head
   float scale;

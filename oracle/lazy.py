@@ -121,3 +121,41 @@ def lazy_backward(q, k, v, bias, tau, do, window=None, varlen=None):
             dk[b, :, n:] = 0.0
             dv[b, :, n:] = 0.0
     return dq, dk, dv, dbias, dtau
+
+
+def lazy_weights(q, k, bias, tau, window=None, varlen=None):
+    """e [B, H, L, L] = relu(p + tau/(i+1)) on valid (j <= i, j < varlen) entries, 0 elsewhere
+    and on rows i >= varlen; with `margin` [B, H, L, L] = |p + tau/(i+1)| for tie detection."""
+    q, k = (np.asarray(t, dtype=np.float64) for t in (q, k))
+    bias = np.asarray(bias, dtype=np.float64)
+    tau = np.asarray(tau, dtype=np.float64)
+    if window is None:
+        window = bias.shape[1]
+    B, H, L, _ = q.shape
+    e = np.zeros((B, H, L, L))
+    margin = np.full((B, H, L, L), np.inf)
+    for b in range(B):
+        n = L if varlen is None else int(varlen[b])
+        for h in range(H):
+            s, valid, keyok, _, _ = _scores(q, k, bias, window, varlen, b, h, L)
+            ok = valid & keyok
+            sm = np.where(ok, s, -np.inf)
+            mx = sm.max(-1, keepdims=True)
+            lse = mx + np.log(np.exp(sm - mx).sum(-1, keepdims=True))
+            pt = np.exp(sm - lse) + tau[h] / np.arange(1, L + 1)[:, None]
+            w = np.where(ok, np.maximum(pt, 0.0), 0.0)
+            w[n:] = 0.0
+            e[b, h] = w
+            margin[b, h] = np.where(ok, np.abs(pt), np.inf)
+            margin[b, h, n:] = np.inf
+    return e, margin
+
+
+def lazy_block_mask(e, block=64):
+    """bool [B, H, ceil(L/block), ceil(L/block)]: block (r, c) holds some e > 0 -- the block
+    sparsity planned at CURSOR_TASKS.md:214-245 (BLOCK_M = BLOCK_N = 64)."""
+    B, H, L, _ = e.shape
+    nb = -(-L // block)
+    pad = nb * block - L
+    ep = np.pad(e > 0, ((0, 0), (0, 0), (0, pad), (0, pad)))
+    return ep.reshape(B, H, nb, block, nb, block).any(axis=(3, 5))

@@ -9,7 +9,7 @@ import pytest
 import torch
 
 from _gpu_util import DEV, assert_close, banner, rand, to_np
-from oracle.lazy import lazy_backward, lazy_forward
+from oracle.lazy import lazy_backward, lazy_block_mask, lazy_forward, lazy_weights
 
 pytestmark = pytest.mark.gpu
 
@@ -149,3 +149,45 @@ def test_bf16_bias_and_tau_dtypes():
     assert_close(to_np(out), ref, 2e-2, "bf16 params forward")
     out.sum().backward()
     assert ts[3].grad.dtype == torch.bfloat16 and ts[4].grad.dtype == torch.bfloat16
+
+
+@pytest.mark.parametrize("tauval", [-1.0, -0.3, 0.3, -10.0])
+@pytest.mark.parametrize("varlen", [None, [150, 260]])
+def test_block_mask_vs_oracle(tauval, varlen):
+    # Block sparsity planned at CURSOR_TASKS.md:214-312: 64x64 blocks with some relu(p + tau/i) > 0.
+    banner("lazy block mask", tauval, varlen)
+    B, H, L, D, W = 2, 2, 260, 32, 40
+    q, k, v, bias, tau = _case(B, H, L, D, W, torch.float32, seed=31, tau=tauval)
+    e, margin = lazy_weights(to_np(q), to_np(k), to_np(bias), to_np(tau), W, varlen)
+    sure = lazy_block_mask(np.where(margin > 1e-6, e, 0.0))  # blocks with a weight clearly > 0
+    maybe = lazy_block_mask(np.where(margin <= 1e-6, 1.0, e))  # ... or a near-tie
+    vl = None if varlen is None else torch.tensor(varlen, dtype=torch.int32, device=DEV)
+    args = [t.to(DEV) for t in (q, k, v, bias, tau)]
+    out_m, bm = _op()(*args, window_size=W, varlen=vl, return_mask=True)
+    out = _op()(*args, window_size=W, varlen=vl)
+    got = bm.cpu().numpy()
+    assert got.shape == sure.shape and got.dtype == np.bool_
+    assert (got >= sure).all() and (got <= maybe).all(), "block mask differs from the oracle"
+    assert torch.equal(out_m, out)  # skipped tiles contribute exactly zero
+    if tauval == -10.0:
+        from adasplash import get_sparsity_stats
+
+        st = get_sparsity_stats(bm)
+        assert st["block_density"] < 0.5 and st["theoretical_speedup"] > 2.0
+
+
+def test_block_mask_with_autograd():
+    q, k, v, bias, tau = _case(1, 2, 200, 64, 32, torch.float32, seed=12, tau=-0.5)
+    do = rand((1, 2, 200, 64), torch.float32, 13)
+    grads = []
+    for want in (False, True):
+        ts = [t.to(DEV).requires_grad_(True) for t in (q, k, v, bias, tau)]
+        res = _op()(*ts, window_size=32, return_mask=want)
+        out = res[0] if want else res
+        if want:
+            assert res[1].dtype == torch.bool and not res[1].requires_grad
+        out.backward(do.to(DEV))
+        grads.append([t.grad.clone() for t in ts])
+    for a, b, n in zip(*grads, ("dq", "dk", "dv", "dbias", "dtau")):
+        # dbias / dtau sum per-tile partials built with LDS float atomics: equal up to order
+        assert torch.equal(a, b) if n in ("dq", "dk", "dv") else torch.allclose(a, b, rtol=1e-5, atol=1e-6), n

@@ -4,6 +4,10 @@ Checks: torch float64 autograd through a restatement of compare_scratch_flash.py
 (the reference's vectorised scratch implementation, with the kernel's 0 <= d < W bias
 window, lazy_attention_triton.py:62), tau = 0 reducing to causal softmax attention with
 bias, tau = -100 giving zero output (tests/test_lazy_attention.py:28-52), varlen zero rows.
+Block mask: the attention weights agree with the torch restatement, tau = -100 gives an
+empty mask, tau > 0 gives exactly the causally visible blocks of the valid rows/keys (every
+visible weight is then > 0), and the output recomputed from the masked blocks alone is the
+full output (no non-zero weight lies outside the mask).
 """
 import math
 
@@ -11,7 +15,7 @@ import numpy as np
 import pytest
 import torch
 
-from oracle.lazy import lazy_backward, lazy_forward
+from oracle.lazy import lazy_backward, lazy_block_mask, lazy_forward, lazy_weights
 
 
 def _torch_lazy(q, k, v, bias, tau, W, varlen=None):
@@ -88,3 +92,49 @@ def test_tau_very_negative_gives_zero():
     q, k, v = (rng.standard_normal((1, 1, 10, 8)) for _ in range(3))
     out = lazy_forward(q, k, v, np.zeros((1, 4)), np.array([-100.0]), 4)
     assert np.abs(out).max() < 1e-12
+
+
+def _torch_weights(q, k, bias, tau, W, varlen=None):
+    B, H, L, D = q.shape
+    s = q @ k.transpose(-1, -2) * D ** -0.5
+    rel = torch.arange(L)[:, None] - torch.arange(L)[None, :]
+    s = s + bias[:, rel.clamp(0, bias.shape[1] - 1)] * ((0 <= rel) & (rel < W))
+    keep = torch.tril(torch.ones(L, L, dtype=torch.bool))[None, None].expand(B, H, L, L).clone()
+    rowv = torch.ones(B, 1, L, 1, dtype=torch.bool)
+    if varlen is not None:
+        ar = torch.arange(L)
+        keep &= (ar[None, :] < torch.as_tensor(varlen)[:, None])[:, None, None, :]
+        rowv = (ar[None, :] < torch.as_tensor(varlen)[:, None])[:, None, :, None]
+    w = torch.softmax(s.masked_fill(~keep, float("-inf")), -1)
+    w = torch.relu(w + tau.view(1, H, 1, 1) / torch.arange(1, L + 1, dtype=q.dtype).view(1, 1, -1, 1))
+    return w.masked_fill(~keep, 0).masked_fill(~rowv, 0)
+
+
+@pytest.mark.parametrize("varlen", [None, [70, 130]])
+def test_block_mask_properties(varlen):
+    rng = np.random.default_rng(7)
+    B, H, L, D, W = 2, 3, 130, 16, 20
+    q, k, v = (rng.standard_normal((B, H, L, D)) for _ in range(3))
+    bias = rng.standard_normal((H, W)) * 0.3
+    tau = np.array([-1.0, -0.05, 0.4])
+    e, margin = lazy_weights(q, k, bias, tau, W, varlen)
+    ref_w = _torch_weights(*(torch.from_numpy(x) for x in (q, k, bias, tau)), W, varlen).numpy()
+    assert np.abs(e - ref_w).max() < 1e-12
+    m = lazy_block_mask(e)
+    assert m.shape == (B, H, 3, 3)
+    # output from the masked blocks alone equals the full output
+    bm = np.repeat(np.repeat(m, 64, axis=2), 64, axis=3)[:, :, :L, :L]
+    out = lazy_forward(q, k, v, bias, tau, W, varlen)
+    assert np.abs(np.where(bm, e, 0.0) @ v - out).max() < 1e-12
+    # tau > 0: every visible (row < len, key <= row, key < len) block is set
+    n = [L, L] if varlen is None else varlen
+    for b in range(B):
+        vis = np.zeros((3, 3), dtype=bool)
+        for r in range(3):
+            for c in range(3):
+                vis[r, c] = 64 * r < n[b] and 64 * c < n[b] and c <= r
+        assert (m[b, 2] == vis).all()
+    # tau = -100: nothing survives
+    e0, _ = lazy_weights(q, k, bias, np.full(H, -100.0), W, varlen)
+    assert not lazy_block_mask(e0).any()
+    assert np.isfinite(margin[e > 0]).all()
