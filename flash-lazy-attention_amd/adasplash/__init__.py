@@ -6,7 +6,7 @@ and the ``LazyAttention`` layer (``adasplash.lazy_attention``, tests/test_lazy_a
 """
 from .adasplash_block_mask import adasplash, adasplash_stats
 from .adasplash_no_block_mask import adasplash_no_block_mask
-from .lazy_attention import LazyAttention, RotaryEmbedding
+from .lazy_attention import LazyAttention, LazyKVCache, RotaryEmbedding
 from .lazy_attention_triton import LazyAttentionTritonFunc, get_sparsity_stats, lazy_attention_triton
 from .triton_entmax import triton_entmax
 
@@ -20,4 +20,5 @@ __all__ = [
     "get_sparsity_stats",
     "LazyAttention",
     "RotaryEmbedding",
+    "LazyKVCache",
 ]

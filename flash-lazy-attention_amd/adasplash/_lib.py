@@ -48,6 +48,11 @@ SIGNATURES = {
     ),
     "fla_lazy_fwd": ([_T4, _T4, _T4, _T4, _P, _I64, _P, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I, _F, _P], _I),
     "fla_lazy_bwd_workspace_size": ([_I, _I, _I, _I], ctypes.c_size_t),
+    "fla_lazy_decode_workspace_size": ([_I, _I, _I, _I, _I, _I], ctypes.c_size_t),
+    "fla_lazy_decode_fwd": (
+        [_T4, _T4, _T4, _T4, _P, _I64, _P, _I, _P, _P, ctypes.c_size_t, _I, _I, _I, _I, _I, _I, _I, _F, _P],
+        _I,
+    ),
     "fla_lazy_bwd": (
         [_T4, _T4, _T4, _T4, _T4, _T4, _T4, _P, _I64, _P, _I, _P, _P, _P, _P, _P, _P, ctypes.c_size_t,
          _I, _I, _I, _I, _I, _I, _F, _P],
@@ -122,7 +127,7 @@ def prep_bhld(x, Dk):
     return x
 
 
-def check_inputs(q, k, v):
+def check_inputs(q, k, v, kv_longer=False):
     if not (q.is_cuda and k.is_cuda and v.is_cuda):
         raise ValueError("q, k, v must be GPU tensors")
     if q.dtype not in DTYPE_CODE:
@@ -133,7 +138,8 @@ def check_inputs(q, k, v):
         raise ValueError(f"expected [B, H, L, D] q and matching k, v; got {tuple(q.shape)}, {tuple(k.shape)}, "
                          f"{tuple(v.shape)}")
     B, H, L, D = q.shape
-    if k.shape[0] != B or k.shape[2] != L or k.shape[3] != D or k.shape[1] <= 0 or H % k.shape[1]:
+    okL = k.shape[2] >= L if kv_longer else k.shape[2] == L
+    if k.shape[0] != B or not okL or k.shape[3] != D or k.shape[1] <= 0 or H % k.shape[1]:
         raise ValueError(f"k, v must be [B, H_kv, L, D] with H_kv dividing H={H}; got {tuple(k.shape)}")
     return D, 1.0 / math.sqrt(D)
 

@@ -8,6 +8,10 @@ parameter conventions follow the reference's layer example (examples/lazy_attent
 34-90): q/k/v/o projections without output bias, fp32 ``tau`` initialised to -1, fp32 biases
 initialised to 0, rotate-half RoPE with base ``rope_base``, grouped K/V heads.
 
+With a ``LazyKVCache`` the layer also decodes: the cached (rotated) keys and values are
+attended by the new positions through the KV-cache kernels (the layer example's
+past_key_values path, examples/lazy_attention_layer.py:133-144).
+
 The attention itself is the HIP kernel pair behind ``lazy_attention_triton``: inputs must be
 GPU tensors (a CPU input raises, there is no PyTorch fallback).  K/V heads are read in place
 for grouped-query attention (no repeat_interleave, unlike examples/sw_attention_lazy.py:154).
@@ -53,6 +57,25 @@ class RotaryEmbedding(nn.Module):
         return rot(q), rot(k)
 
 
+class LazyKVCache:
+    """Preallocated K/V cache [B, H_kv, max_len, D] for LazyAttention decoding (rotated keys)."""
+
+    def __init__(self, batch, num_kv_heads, max_len, head_dim, device=None, dtype=torch.float32):
+        self.k = torch.zeros(batch, num_kv_heads, max_len, head_dim, device=device, dtype=dtype)
+        self.v = torch.zeros_like(self.k)
+        self.len = 0
+
+    def append(self, k, v):
+        """k, v [B, H_kv, L, D] -> views of the whole cache so far."""
+        L = k.shape[2]
+        if self.len + L > self.k.shape[2]:
+            raise ValueError("KV cache is full")
+        self.k[:, :, self.len:self.len + L] = k
+        self.v[:, :, self.len:self.len + L] = v
+        self.len += L
+        return self.k[:, :, :self.len], self.v[:, :, :self.len]
+
+
 class LazyAttention(nn.Module):
     def __init__(self, dim, num_heads, window_size=512, rope_base=10000.0, num_kv_heads=None, qkv_bias=False):
         super().__init__()
@@ -75,15 +98,26 @@ class LazyAttention(nn.Module):
         self.attention_biases = nn.Parameter(torch.zeros(num_heads, window_size, dtype=torch.float32))
         self.tau = nn.Parameter(torch.full((num_heads,), -1.0, dtype=torch.float32))
 
-    def forward(self, x, varlen=None):
+    def new_cache(self, batch, max_len, device=None, dtype=None):
+        w = self.q_proj.weight
+        return LazyKVCache(batch, self.num_kv_heads, max_len, self.head_dim, device or w.device, dtype or w.dtype)
+
+    def forward(self, x, varlen=None, cache=None):
         """x: [B, L, dim] -> [B, L, dim].  varlen: optional [B] true lengths (right padding);
-        output rows at positions >= varlen[b] are zero before the output projection."""
+        output rows at positions >= varlen[b] are zero before the output projection.
+        cache: optional LazyKVCache; x then holds the next L positions after the cached ones
+        (prefill when the cache is empty, decode steps after that; inference only)."""
         B, L, _ = x.shape
         q = self.q_proj(x).view(B, L, self.num_heads, self.head_dim)
         k = self.k_proj(x).view(B, L, self.num_kv_heads, self.head_dim)
         v = self.v_proj(x).view(B, L, self.num_kv_heads, self.head_dim)
-        q, k = self.rotary(q, k)
+        offset = 0 if cache is None else cache.len
+        q, k = self.rotary(q, k, offset)
         # [B, L, H, D] -> [B, H, L, D] as strided views; the op reads them in place
-        o = lazy_attention_triton(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),
-                                  self.attention_biases, self.tau, window_size=self.window_size, varlen=varlen)
+        q, k, v = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
+        if cache is not None:
+            if varlen is not None:
+                raise ValueError("varlen is not supported together with a KV cache")
+            k, v = cache.append(k, v)
+        o = lazy_attention_triton(q, k, v, self.attention_biases, self.tau, window_size=self.window_size, varlen=varlen)
         return self.o_proj(o.transpose(1, 2).reshape(B, L, self.dim))

@@ -117,9 +117,41 @@ class LazyAttentionTritonFunc(torch.autograd.Function):
         return dq, dk, dv, dbias, dtau, None, None, None
 
 
+def _decode_forward(q, k, v, bias, tau, window_size, varlen):
+    """q [B, H, Lq, D] at the last Lq positions of each sequence against the cache k, v
+    [B, H_kv, Lk, D] (Lq < Lk); varlen = cache lengths [B].  Inference only."""
+    D, scale = check_inputs(q, k, v, kv_longer=True)
+    Dk = kernel_head_dim(D)
+    qp, kp, vp = (prep_bhld(x, Dk) for x in (q, k, v))
+    B, H, Lq, _ = qp.shape
+    Hkv, Lk = kp.shape[1], kp.shape[2]
+    b32, t32, W = _params(bias, tau, H, window_size)
+    vl = prep_varlen(varlen, B, q.device)
+    out = torch.empty((B, H, Lq, Dk), device=q.device, dtype=q.dtype)
+    nbytes = int(lib().fla_lazy_decode_workspace_size(B, H, Hkv, Lq, Lk, Dk))
+    if nbytes == 0:
+        raise ValueError(f"unsupported decode shape q {tuple(q.shape)}, k {tuple(k.shape)}")
+    ws = torch.empty((nbytes,), device=q.device, dtype=torch.uint8)
+    rc = lib().fla_lazy_decode_fwd(
+        t4(qp), t4(kp), t4(vp), t4(out), ptr(b32), b32.shape[1], ptr(t32), W, ptr(vl), ptr(ws), nbytes,
+        B, H, Hkv, Lq, Lk, Dk, DTYPE_CODE[q.dtype], scale, stream_of(q),
+    )
+    check(rc, "fla_lazy_decode_fwd")
+    return out[..., :D] if Dk != D else out
+
+
 def lazy_attention_triton(q, k, v, bias, tau, window_size=None, varlen=None, return_mask=False):
+    """See the module docstring.  With q shorter than k, v (a KV cache: q holds the last
+    q.shape[2] positions of each sequence, varlen the cache lengths) the inference-only decode
+    kernels run instead; they produce no gradient."""
     if window_size is None:
         window_size = bias.shape[1]
+    if q.dim() == 4 and k.dim() == 4 and q.shape[2] < k.shape[2]:
+        if return_mask:
+            raise ValueError("return_mask is not available on the KV-cache path")
+        if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v, bias, tau)):
+            raise NotImplementedError("the KV-cache (Lq < Lk) path is inference only; wrap it in torch.no_grad()")
+        return _decode_forward(q, k, v, bias, tau, window_size, varlen)
     if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v, bias, tau)):
         return LazyAttentionTritonFunc.apply(q, k, v, bias, tau, window_size, varlen, bool(return_mask))
     res = _forward(q, k, v, bias, tau, window_size, varlen, False, bool(return_mask))

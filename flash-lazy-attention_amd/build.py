@@ -25,6 +25,9 @@ SOURCES = [
     "lazy_f32.hip",
     "lazy_f16.hip",
     "lazy_bf16.hip",
+    "lazy_dec_f32.hip",
+    "lazy_dec_f16.hip",
+    "lazy_dec_bf16.hip",
 ]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [

@@ -234,3 +234,80 @@ extern "C" int fla_lazy_bwd(const fla_tensor4_t* q, const fla_tensor4_t* k, cons
   FLA_DISPATCH(lazy_bwd_launch, a, s)
   return (int)e;
 }
+
+namespace {
+
+// Decode work split: query rows in groups of RG (1, 2, 4 or 8), keys in chunks of a multiple of
+// 64 chosen so that units x chunks gives about 1024 workgroups.
+struct DecPlan {
+  int G, RG, nrg, nsplit, chunk;
+  size_t ml_bytes, po_bytes;
+};
+
+bool dec_plan(int B, int H, int Hkv, int Lq, int Lk, int D, DecPlan& p) {
+  if (B <= 0 || H <= 0 || Hkv <= 0 || H % Hkv || Lq <= 0 || Lk <= 0 || Lk > (1 << 24)) return false;
+  if (D != 32 && D != 64 && D != 128) return false;
+  p.G = H / Hkv;
+  const int64_t R = (int64_t)p.G * Lq;
+  if (R > (1 << 20)) return false;
+  p.RG = R >= 8 ? 8 : R >= 4 ? 4 : R >= 2 ? 2 : 1;
+  p.nrg = (int)((R + p.RG - 1) / p.RG);
+  const int64_t units = (int64_t)B * Hkv * p.nrg;
+  const int64_t maxsplit = (Lk + 255) / 256;
+  int64_t ns = (1024 + units - 1) / units;
+  ns = ns < 1 ? 1 : (ns > maxsplit ? maxsplit : ns);
+  p.chunk = (int)(((Lk + ns - 1) / ns + 63) / 64 * 64);
+  p.nsplit = (Lk + p.chunk - 1) / p.chunk;
+  if (units * p.nsplit > 0x7fffffffLL) return false;
+  auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
+  p.ml_bytes = up((size_t)units * p.nsplit * p.RG * 2 * 4);
+  p.po_bytes = up((size_t)units * p.nsplit * p.RG * D * 4);
+  return true;
+}
+
+}  // namespace
+
+extern "C" size_t fla_lazy_decode_workspace_size(int B, int H, int Hkv, int Lq, int Lk, int D) {
+  DecPlan p;
+  if (!dec_plan(B, H, Hkv, Lq, Lk, D, p)) return 0;
+  return p.ml_bytes + p.po_bytes;
+}
+
+extern "C" int fla_lazy_decode_fwd(const fla_tensor4_t* q, const fla_tensor4_t* k, const fla_tensor4_t* v,
+                                   const fla_tensor4_t* out, const float* bias, int64_t bias_ld, const float* tau,
+                                   int window, const int32_t* varlen, void* workspace, size_t workspace_bytes, int B,
+                                   int H, int Hkv, int Lq, int Lk, int D, int dtype, float scale, void* stream) {
+  DecPlan p;
+  if (!dec_plan(B, H, Hkv, Lq, Lk, D, p)) return FLA_EINVAL;
+  if (dtype != FLA_F32 && dtype != FLA_F16 && dtype != FLA_BF16) return FLA_EUNSUPPORTED;
+  if (!good_tensor(q, dtype) || !good_tensor(k, dtype) || !good_tensor(v, dtype) || !good_tensor(out, dtype))
+    return FLA_EINVAL;
+  if (!bias || !tau || window <= 0 || bias_ld < window || !(scale > 0.0f)) return FLA_EINVAL;
+  if (!workspace || workspace_bytes < p.ml_bytes + p.po_bytes || ((uintptr_t)workspace) % 256) return FLA_EWORKSPACE;
+  LazyDecArgs a = {};
+  a.q = T4(q);
+  a.k = T4(k);
+  a.v = T4(v);
+  a.o = T4(out);
+  a.bias = bias;
+  a.bias_ld = bias_ld;
+  a.tau = tau;
+  a.varlen = varlen;
+  a.ml = (float*)workspace;
+  a.po = (float*)((char*)workspace + p.ml_bytes);
+  a.B = B;
+  a.H = H;
+  a.G = p.G;
+  a.Lq = Lq;
+  a.Lk = Lk;
+  a.W = window;
+  a.RG = p.RG;
+  a.nrg = p.nrg;
+  a.nsplit = p.nsplit;
+  a.chunk = p.chunk;
+  a.scale = scale;
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e;
+  FLA_DISPATCH(lazy_decode_launch, a, s)
+  return (int)e;
+}

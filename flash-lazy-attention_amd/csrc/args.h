@@ -51,6 +51,21 @@ struct LazyArgs {
   float scale;
 };
 
+// KV-cache (decode) forward of lazy attention.  A unit is (b, K/V head, group of RG query
+// rows); row r of K/V head hk is query position r % Lq of query head hk*G + r / Lq.
+struct LazyDecArgs {
+  Tensor4 q, k, v, o;      // q, o [B, H, Lq, D]; k, v [B, H/G, Lk, D]
+  const float* bias;       // fp32 [H, bias_ld]
+  int64_t bias_ld;
+  const float* tau;        // fp32 [H]
+  const int32_t* varlen;   // [B] cache lengths, optional (else Lk)
+  float* ml;               // [units, nsplit, RG, 2] per-chunk (max, sum exp2) scratch
+  float* po;               // [units, nsplit, RG, D] per-chunk output scratch
+  int B, H, G, Lq, Lk, W;
+  int RG, nrg, nsplit, chunk;
+  float scale;
+};
+
 template <int DT, int D>
 hipError_t ada_fwd_launch(const AdaFwdArgs& a, int mode, hipStream_t s);
 template <int DT, int D>
@@ -59,5 +74,8 @@ template <int DT, int D>
 hipError_t lazy_fwd_launch(const LazyArgs& a, hipStream_t s);
 template <int DT, int D>
 hipError_t lazy_bwd_launch(const LazyArgs& a, hipStream_t s);
+
+template <int DT, int D>
+hipError_t lazy_decode_launch(const LazyDecArgs& a, hipStream_t s);
 
 }  // namespace fla

@@ -117,6 +117,21 @@ int fla_lazy_bwd(const fla_tensor4_t* q, const fla_tensor4_t* k, const fla_tenso
                  const int32_t* varlen, float* dbias, float* dtau, void* workspace, size_t workspace_bytes, int B,
                  int H, int Hkv, int L, int D, int dtype, float scale, void* stream);
 
+/* Bytes of caller-provided scratch for fla_lazy_decode_fwd (0 for invalid sizes). */
+size_t fla_lazy_decode_workspace_size(int B, int H, int Hkv, int Lq, int Lk, int D);
+
+/* Lazy attention over a KV cache (inference forward; decode and chunked prefill).  q, out are
+ * [B, H, Lq, D]; k, v are the cache [B, Hkv, Lk, D].  Query i of batch b sits at position
+ * pos = len_b - Lq + i (len_b = varlen[b] if given, else Lk) and attends to keys j <= pos,
+ * j < len_b with the weights of fla_lazy_fwd at that position: relu(softmax(s + bias[h, pos-j]
+ * for 0 <= pos-j < window) + tau_h/(pos+1)).  Rows with pos < 0 are zero.  This is the call the
+ * reference's layer makes with a cache (examples/lazy_attention_layer.py:133-169), which its
+ * square kernel (Lq = Lk assumed) does not cover.  No lse / backward state is produced. */
+int fla_lazy_decode_fwd(const fla_tensor4_t* q, const fla_tensor4_t* k, const fla_tensor4_t* v,
+                        const fla_tensor4_t* out, const float* bias, int64_t bias_ld, const float* tau, int window,
+                        const int32_t* varlen, void* workspace, size_t workspace_bytes, int B, int H, int Hkv, int Lq,
+                        int Lk, int D, int dtype, float scale, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

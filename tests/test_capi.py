@@ -26,7 +26,8 @@ def _declared():
 def test_header_declares_the_abi():
     names = _declared()
     for n in ("fla_entmax_fwd", "fla_entmax_bwd", "fla_adasplash_fwd", "fla_adasplash_bwd", "fla_lazy_fwd",
-              "fla_lazy_bwd", "fla_lazy_bwd_workspace_size", "fla_adasplash_mask_words", "fla_version"):
+              "fla_lazy_bwd", "fla_lazy_bwd_workspace_size", "fla_adasplash_mask_words", "fla_version",
+              "fla_lazy_decode_fwd", "fla_lazy_decode_workspace_size"):
         assert n in names
 
 
@@ -35,6 +36,15 @@ def test_every_declared_symbol_is_exported():
     for n in _declared():
         assert hasattr(lib, n), n
         assert n in L.SIGNATURES, f"{n} has no ctypes signature"
+
+
+def test_decode_workspace_plan():
+    L, lib = _lib()
+    assert lib.fla_lazy_decode_workspace_size(2, 8, 2, 1, 4096, 64) > 0
+    assert lib.fla_lazy_decode_workspace_size(2, 8, 3, 1, 4096, 64) == 0  # H % Hkv != 0
+    assert lib.fla_lazy_decode_workspace_size(2, 8, 2, 1, 4096, 48) == 0  # not a kernel head dim
+    # more query rows per K/V head never shrink the scratch
+    assert lib.fla_lazy_decode_workspace_size(1, 8, 1, 4, 1000, 64) >= lib.fla_lazy_decode_workspace_size(1, 8, 1, 1, 1000, 64)
 
 
 def test_pure_helpers():
