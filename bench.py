@@ -33,7 +33,7 @@ PEAK_HBM_GBPS = 8000.0
 # HBM bytes per launch of ada_fwd_kernel at the headline config, from two rocprofv3 --pmc
 # passes (FETCH_SIZE x2.000, WRITE_SIZE x1.000 after calibration on a plain 256 MiB copy);
 # source: profiles/adasplash_causal_L8192_a15_traffic.txt.
-FWD_TRAFFIC_BYTES = (131181 * 2.0 + 99397 * 1.0) * 1024
+FWD_TRAFFIC_BYTES = (126085 * 2.0 + 99386 * 1.0) * 1024
 
 
 def dense_flops(B, H, L, D, causal=True):
@@ -204,6 +204,27 @@ def bench_configs(dev, steps, warmup):
     res["cfg5_lazy_fwd_ms"] = msf
     lvl = torch.randint(L // 8, L + 1, (B,), generator=torch.Generator().manual_seed(1)).to(dev)
     res["cfg5_lazy_varlen_ms"] = time_region(run_lazy(lvl.to(torch.int32)), steps, warmup)
+    # block-sparse lazy forward (return_mask: 64x64 blocks with relu(p + tau/i) > 0, empty ones skipped)
+    from adasplash import get_sparsity_stats
+
+    with torch.no_grad():
+        for tv in (-1.0, -10.0):
+            tt = torch.full((H,), tv, device=dev)
+            _o, bm = lazy_attention_triton(q, k, v, bias, tt, window_size=W, return_mask=True)
+            res[f"cfg5_lazy_tau{int(tv)}_visible_block_density"] = get_sparsity_stats(bm)["visible_density"]
+            res[f"cfg5_lazy_tau{int(tv)}_fwd_ms_dense"] = time_region(
+                lambda: lazy_attention_triton(q, k, v, bias, tt, window_size=W), steps, warmup)
+            res[f"cfg5_lazy_tau{int(tv)}_fwd_ms_blocksparse"] = time_region(
+                lambda: lazy_attention_triton(q, k, v, bias, tt, window_size=W, return_mask=True), steps, warmup)
+    del q, k, v, do, qr, kr, vr
+    # KV-cache decode (one new token, GQA 32 query heads over 8 K/V heads, 8192 cached keys)
+    Bd, Hd, Hkv, Lk = 8, 32, 8, 8192
+    qd, kd, vd = rnd(Bd, Hd, 1, D), rnd(Bd, Hkv, Lk, D), rnd(Bd, Hkv, Lk, D)
+    bd, td = torch.zeros(Hd, W, device=dev), torch.full((Hd,), -1.0, device=dev)
+    with torch.no_grad():
+        ms = time_region(lambda: lazy_attention_triton(qd, kd, vd, bd, td, window_size=W), steps, warmup)
+    res["decode_lazy_gqa_us"] = ms * 1e3
+    res["decode_lazy_gqa_kv_GBps"] = 2 * kd.numel() * 2 / (ms * 1e-3) / 1e9  # K and V read once (algorithmic)
     return res
 
 
@@ -265,8 +286,8 @@ def cpu_baseline(shape, budget_s=12.0):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline step only (for profiling runs)")
     ap.add_argument("--calib-copy", action="store_true",
