@@ -256,6 +256,10 @@ struct RowTile {
 
 // Same, stored transposed as [D][ROWS] (row stride LDT).  16-bit types move two source rows
 // per thread so every LDS write is one packed 32-bit (row, row+1) pair (one v_perm_b32 each).
+// For 16-bit types the rows of every group of 16 are stored in the order 0-3, 8-11, 4-7,
+// 12-15 (bits 2 and 3 of the row index swapped): the 8 rows one MFMA fragment pairs with
+// accumulator registers (row_of) are then contiguous and load_perm_frag reads them with a
+// single 16-byte access.
 template <typename T, int ROWS, int D, int LDT>
 struct TransTile {
   static constexpr int EPV = 16 / sizeof(T);
@@ -297,12 +301,13 @@ struct TransTile {
       if (u >= NU) continue;
       if constexpr (PAIR) {
         const int kp = u % (ROWS / 2), col = (u / (ROWS / 2)) * EPV;
+        const int k = 2 * kp, pos = (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1);
         const uint32_t a4[4] = {r0[i].x, r0[i].y, r0[i].z, r0[i].w};
         const uint32_t b4[4] = {r1[i].x, r1[i].y, r1[i].z, r1[i].w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          *reinterpret_cast<uint32_t*>(lds + (col + 2 * e) * LDT + 2 * kp) = __builtin_amdgcn_perm(b4[e], a4[e], 0x05040100u);
-          *reinterpret_cast<uint32_t*>(lds + (col + 2 * e + 1) * LDT + 2 * kp) = __builtin_amdgcn_perm(b4[e], a4[e], 0x07060302u);
+          *reinterpret_cast<uint32_t*>(lds + (col + 2 * e) * LDT + pos) = __builtin_amdgcn_perm(b4[e], a4[e], 0x05040100u);
+          *reinterpret_cast<uint32_t*>(lds + (col + 2 * e + 1) * LDT + pos) = __builtin_amdgcn_perm(b4[e], a4[e], 0x07060302u);
         }
       } else {
         const int row = u % ROWS, col = (u / ROWS) * EPV;
@@ -322,10 +327,8 @@ template <int DT>
 __device__ __forceinline__ typename Tr<DT>::frag load_perm_frag(const typename Tr<DT>::T* row, int j, int g) {
   typedef typename Tr<DT>::frag frag;
   if constexpr (Tr<DT>::KPL == 8) {
-    uint2 lo = *reinterpret_cast<const uint2*>(row + 16 * j + 4 * g);
-    uint2 hi = *reinterpret_cast<const uint2*>(row + 16 * j + 8 + 4 * g);
-    uint4 w = make_uint4(lo.x, lo.y, hi.x, hi.y);
-    return __builtin_bit_cast(frag, w);
+    // rows 16j+4g+(0..3) and 16j+8+4g+(0..3), stored contiguously by TransTile
+    return __builtin_bit_cast(frag, *reinterpret_cast<const uint4*>(row + 16 * j + 8 * g));
   } else {
     return row[row_of(j, g)];
   }
@@ -364,13 +367,12 @@ __device__ __forceinline__ void store_acc_row(typename Tr<DT>::T* rowp, const f3
 static constexpr int LDS_LIMIT = 160 * 1024;
 
 // Row padding (elements) of LDS tiles stored transposed ([D][64]) and read back with
-// load_perm_frag.  Those reads are 8 bytes per lane for 16-bit types (4 bytes for fp32) from
-// 32 consecutive rows; a row stride of 34 (resp. 65) dwords puts the rows of one read on
-// distinct banks, where the 16-byte padding of the row-major tiles (36 dwords) would
-// make rows r and r+8 collide.
+// load_perm_frag: 16-byte reads per lane for 16-bit types, so rows stay 16-byte aligned
+// (a 36-dword stride puts 8 consecutive rows of one read on distinct banks); fp32 reads are
+// 4 bytes per lane from 32 rows, and a 65-dword stride spreads those over the banks.
 template <typename T>
 struct TransPad {
-  static constexpr int value = sizeof(T) == 2 ? 4 : 1;
+  static constexpr int value = sizeof(T) == 2 ? 8 : 1;
 };
 template <int DT>
 struct Occ {
