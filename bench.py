@@ -122,11 +122,20 @@ def bench_entmax(dev, iters=200):
     x = torch.randn(128, 256, generator=g).to(dev)
     ms = time_region(lambda: triton_entmax(x, alpha=1.5, n_iter=10, fast_math=True), iters, 10)
     nbytes = 2 * 4 * 128 * 256
+    # the kernel alone: one C-ABI call per iteration with prebuilt ctypes arguments
+    from adasplash import _lib as L_
+
+    y = torch.empty_like(x)
+    fn, args = L_.lib().fla_entmax_fwd, (L_.ptr(x), L_.ptr(y), 128, 256, 256, 256, L_.FLA_F32, 1.5, 10, 1,
+                                         L_.stream_of(x))
+    ms_k = time_region(lambda: fn(*args), iters, 10)
     xl = torch.randn(65536, 1024, generator=g).to(dev)
     ms_l = time_region(lambda: triton_entmax(xl, alpha=1.5, n_iter=10, fast_math=True), 20, 3)
     return {
         "entmax_cfg1_us": ms * 1e3,
         "entmax_cfg1_GBps": nbytes / (ms * 1e-3) / 1e9,
+        "entmax_cfg1_kernel_us": ms_k * 1e3,
+        "entmax_cfg1_kernel_GBps": nbytes / (ms_k * 1e-3) / 1e9,
         "entmax_65536x1024_GBps": 2 * 4 * xl.numel() / (ms_l * 1e-3) / 1e9,
     }
 

@@ -11,25 +11,30 @@ import torch
 from ._lib import DTYPE_CODE, check, lib, ptr, stream_of
 
 
+def _forward(x, alpha, n_iter, fast_math):
+    if not x.is_cuda:
+        raise ValueError("triton_entmax expects a GPU tensor")
+    if x.dtype not in DTYPE_CODE:
+        raise TypeError(f"unsupported dtype {x.dtype}")
+    alpha = float(alpha)
+    if not (1.0 < alpha <= 2.0):
+        raise ValueError("alpha must lie in (1, 2]")
+    shape = x.shape
+    n = shape[-1]
+    x2 = x.reshape(-1, n).contiguous()
+    y = torch.empty_like(x2)
+    rc = lib().fla_entmax_fwd(
+        ptr(x2), ptr(y), x2.shape[0], n, n, n, DTYPE_CODE[x.dtype], alpha, int(n_iter), int(bool(fast_math)),
+        stream_of(x2),
+    )
+    check(rc, "fla_entmax_fwd")
+    return y, alpha, shape
+
+
 class EntmaxFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, alpha, n_iter, fast_math):
-        if not x.is_cuda:
-            raise ValueError("triton_entmax expects a GPU tensor")
-        if x.dtype not in DTYPE_CODE:
-            raise TypeError(f"unsupported dtype {x.dtype}")
-        alpha = float(alpha)
-        if not (1.0 < alpha <= 2.0):
-            raise ValueError("alpha must lie in (1, 2]")
-        shape = x.shape
-        n = shape[-1]
-        x2 = x.reshape(-1, n).contiguous()
-        y = torch.empty_like(x2)
-        rc = lib().fla_entmax_fwd(
-            ptr(x2), ptr(y), x2.shape[0], n, n, n, DTYPE_CODE[x.dtype], alpha, int(n_iter), int(bool(fast_math)),
-            stream_of(x2),
-        )
-        check(rc, "fla_entmax_fwd")
+        y, alpha, shape = _forward(x, alpha, n_iter, fast_math)
         ctx.alpha = alpha
         ctx.save_for_backward(y)
         return y.reshape(shape)
@@ -48,4 +53,7 @@ class EntmaxFunction(torch.autograd.Function):
 
 
 def triton_entmax(x, alpha=1.5, n_iter=10, fast_math=True):
-    return EntmaxFunction.apply(x, alpha, n_iter, fast_math)
+    if torch.is_grad_enabled() and x.requires_grad:
+        return EntmaxFunction.apply(x, alpha, n_iter, fast_math)
+    y, _alpha, shape = _forward(x, alpha, n_iter, fast_math)  # no autograd node needed
+    return y.reshape(shape)
