@@ -1,6 +1,8 @@
 // C ABI entry points (declared in include/flashlazy.h): argument validation and dispatch
 // on dtype / head dim / alpha.  Nothing here allocates; all launches are asynchronous on
 // the caller's stream.
+#include <algorithm>
+
 #include "args.h"
 #include "flashlazy_internal.h"
 
@@ -237,20 +239,22 @@ extern "C" int fla_lazy_bwd(const fla_tensor4_t* q, const fla_tensor4_t* k, cons
 
 namespace {
 
-// Decode work split: query rows in groups of RG (1, 2, 4 or 8), keys in chunks of a multiple of
-// 64 chosen so that units x chunks gives about 1024 workgroups.
+// Decode work split: query rows in groups of RG, keys in chunks of a multiple of 64 chosen so
+// that units x chunks gives about 1024 workgroups.  16-bit inputs use the matrix-core kernels
+// (RG = 32); fp32 inputs the vector kernels with RG = 1, 2, 4 or 8.
 struct DecPlan {
-  int G, RG, nrg, nsplit, chunk;
-  size_t ml_bytes, po_bytes;
+  int G, RG, nrg, nsplit, chunk, nsc, Lkp;
+  size_t ml_bytes, po_bytes, sc_bytes;
+  size_t bytes() const { return ml_bytes + po_bytes + sc_bytes; }
 };
 
-bool dec_plan(int B, int H, int Hkv, int Lq, int Lk, int D, DecPlan& p) {
+bool dec_plan(int B, int H, int Hkv, int Lq, int Lk, int D, bool mfma, DecPlan& p) {
   if (B <= 0 || H <= 0 || Hkv <= 0 || H % Hkv || Lq <= 0 || Lk <= 0 || Lk > (1 << 24)) return false;
   if (D != 32 && D != 64 && D != 128) return false;
   p.G = H / Hkv;
   const int64_t R = (int64_t)p.G * Lq;
   if (R > (1 << 20)) return false;
-  p.RG = R >= 8 ? 8 : R >= 4 ? 4 : R >= 2 ? 2 : 1;
+  p.RG = mfma ? 32 : R >= 8 ? 8 : R >= 4 ? 4 : R >= 2 ? 2 : 1;
   p.nrg = (int)((R + p.RG - 1) / p.RG);
   const int64_t units = (int64_t)B * Hkv * p.nrg;
   const int64_t maxsplit = (Lk + 255) / 256;
@@ -262,28 +266,39 @@ bool dec_plan(int B, int H, int Hkv, int Lq, int Lk, int D, DecPlan& p) {
   auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
   p.ml_bytes = up((size_t)units * p.nsplit * p.RG * 2 * 4);
   p.po_bytes = up((size_t)units * p.nsplit * p.RG * D * 4);
+  // Score cache of the matrix-core path: 4 bytes per key and row written and read back instead
+  // of reading a 2*D-byte key row again; kept when that halves the re-read at least (fewer
+  // than D/4 rows per unit, so at most half the size of K).
+  p.nsc = 0;
+  p.Lkp = (Lk + 31) / 32 * 32;
+  if (p.RG == 32) {
+    const int rows = (int)(R < 32 ? R : 32);
+    if (4 * rows < D) p.nsc = rows;
+  }
+  p.sc_bytes = up((size_t)units * p.nsc * p.Lkp * 4);
   return true;
 }
 
 }  // namespace
 
 extern "C" size_t fla_lazy_decode_workspace_size(int B, int H, int Hkv, int Lq, int Lk, int D) {
-  DecPlan p;
-  if (!dec_plan(B, H, Hkv, Lq, Lk, D, p)) return 0;
-  return p.ml_bytes + p.po_bytes;
+  // the larger of the two kernel families' needs, so that the size does not depend on dtype
+  DecPlan p, pm;
+  if (!dec_plan(B, H, Hkv, Lq, Lk, D, false, p) || !dec_plan(B, H, Hkv, Lq, Lk, D, true, pm)) return 0;
+  return std::max(p.bytes(), pm.bytes());
 }
 
 extern "C" int fla_lazy_decode_fwd(const fla_tensor4_t* q, const fla_tensor4_t* k, const fla_tensor4_t* v,
                                    const fla_tensor4_t* out, const float* bias, int64_t bias_ld, const float* tau,
                                    int window, const int32_t* varlen, void* workspace, size_t workspace_bytes, int B,
                                    int H, int Hkv, int Lq, int Lk, int D, int dtype, float scale, void* stream) {
-  DecPlan p;
-  if (!dec_plan(B, H, Hkv, Lq, Lk, D, p)) return FLA_EINVAL;
   if (dtype != FLA_F32 && dtype != FLA_F16 && dtype != FLA_BF16) return FLA_EUNSUPPORTED;
+  DecPlan p;
+  if (!dec_plan(B, H, Hkv, Lq, Lk, D, dtype != FLA_F32, p)) return FLA_EINVAL;
   if (!good_tensor(q, dtype) || !good_tensor(k, dtype) || !good_tensor(v, dtype) || !good_tensor(out, dtype))
     return FLA_EINVAL;
   if (!bias || !tau || window <= 0 || bias_ld < window || !(scale > 0.0f)) return FLA_EINVAL;
-  if (!workspace || workspace_bytes < p.ml_bytes + p.po_bytes || ((uintptr_t)workspace) % 256) return FLA_EWORKSPACE;
+  if (!workspace || workspace_bytes < p.bytes() || ((uintptr_t)workspace) % 256) return FLA_EWORKSPACE;
   LazyDecArgs a = {};
   a.q = T4(q);
   a.k = T4(k);
@@ -295,6 +310,9 @@ extern "C" int fla_lazy_decode_fwd(const fla_tensor4_t* q, const fla_tensor4_t* 
   a.varlen = varlen;
   a.ml = (float*)workspace;
   a.po = (float*)((char*)workspace + p.ml_bytes);
+  a.sc = p.nsc ? (float*)((char*)workspace + p.ml_bytes + p.po_bytes) : nullptr;
+  a.nsc = p.nsc;
+  a.Lkp = p.Lkp;
   a.B = B;
   a.H = H;
   a.G = p.G;

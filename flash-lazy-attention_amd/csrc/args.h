@@ -61,8 +61,10 @@ struct LazyDecArgs {
   const int32_t* varlen;   // [B] cache lengths, optional (else Lk)
   float* ml;               // [units, nsplit, RG, 2] per-chunk (max, sum exp2) scratch
   float* po;               // [units, nsplit, RG, D] per-chunk output scratch
+  float* sc;               // optional [units, nsc, Lkp] base-2 score cache (matrix-core path)
   int B, H, G, Lq, Lk, W;
   int RG, nrg, nsplit, chunk;
+  int nsc, Lkp;            // cached rows per unit, key stride of the cache (Lk rounded up to 32)
   float scale;
 };
 

@@ -222,18 +222,18 @@ __device__ __forceinline__ uint32_t tile_bytes(int64_t ld, int nvalid) {
 // Register-staged tiles for software pipelining: init() fixes each thread's byte offsets once,
 // load() issues the global reads of a tile into registers (rows >= nvalid read as zero),
 // store() writes them to LDS later.
-template <typename T, int ROWS, int D, int LDR>
+template <typename T, int ROWS, int D, int LDR, int NT = 256>
 struct RowTile {
   static constexpr int EPV = 16 / sizeof(T);
   static constexpr int CPR = D / EPV;
   static constexpr int NCH = ROWS * CPR;
-  static constexpr int PER = (NCH + 255) / 256;
+  static constexpr int PER = (NCH + NT - 1) / NT;
   uint4 r[PER];
   uint32_t off[PER];
   __device__ __forceinline__ void init(int64_t ld, int tid) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-      const int c = tid + 256 * i;
+      const int c = tid + NT * i;
       const int row = c / CPR, col = (c % CPR) * EPV;
       off[i] = (uint32_t)(((int64_t)row * ld + col) * sizeof(T));
     }
@@ -242,12 +242,12 @@ struct RowTile {
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(g, tile_bytes<T, D>(ld, min(nvalid, ROWS)));
 #pragma unroll
     for (int i = 0; i < PER; ++i)
-      if (tid + 256 * i < NCH) r[i] = buf_load16(rs, off[i]);
+      if (tid + NT * i < NCH) r[i] = buf_load16(rs, off[i]);
   }
   __device__ __forceinline__ void store(T* __restrict__ lds, int tid) const {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-      const int c = tid + 256 * i;
+      const int c = tid + NT * i;
       const int row = c / CPR, col = (c % CPR) * EPV;
       if (c < NCH) *reinterpret_cast<uint4*>(lds + row * LDR + col) = r[i];
     }
@@ -260,19 +260,19 @@ struct RowTile {
 // 12-15 (bits 2 and 3 of the row index swapped): the 8 rows one MFMA fragment pairs with
 // accumulator registers (row_of) are then contiguous and load_perm_frag reads them with a
 // single 16-byte access.
-template <typename T, int ROWS, int D, int LDT>
+template <typename T, int ROWS, int D, int LDT, int NT = 256>
 struct TransTile {
   static constexpr int EPV = 16 / sizeof(T);
   static constexpr int CPR = D / EPV;
   static constexpr bool PAIR = sizeof(T) == 2;
   static constexpr int NU = PAIR ? (ROWS / 2) * CPR : ROWS * CPR;
-  static constexpr int PER = (NU + 255) / 256;
+  static constexpr int PER = (NU + NT - 1) / NT;
   uint4 r0[PER], r1[PAIR ? PER : 1];
   uint32_t off[PER];
   __device__ __forceinline__ void init(int64_t ld, int tid) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-      const int u = tid + 256 * i;
+      const int u = tid + NT * i;
       int row, col;
       if constexpr (PAIR) {
         row = 2 * (u % (ROWS / 2));
@@ -289,7 +289,7 @@ struct TransTile {
     const uint32_t step = (uint32_t)(ld * sizeof(T));
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-      if (tid + 256 * i >= NU) continue;
+      if (tid + NT * i >= NU) continue;
       r0[i] = buf_load16(rs, off[i]);
       if constexpr (PAIR) r1[i] = buf_load16(rs, off[i] + step);
     }
@@ -297,7 +297,7 @@ struct TransTile {
   __device__ __forceinline__ void store(T* __restrict__ lds, int tid) const {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-      const int u = tid + 256 * i;
+      const int u = tid + NT * i;
       if (u >= NU) continue;
       if constexpr (PAIR) {
         const int kp = u % (ROWS / 2), col = (u / (ROWS / 2)) * EPV;

@@ -43,8 +43,11 @@ def test_decode_workspace_plan():
     assert lib.fla_lazy_decode_workspace_size(2, 8, 2, 1, 4096, 64) > 0
     assert lib.fla_lazy_decode_workspace_size(2, 8, 3, 1, 4096, 64) == 0  # H % Hkv != 0
     assert lib.fla_lazy_decode_workspace_size(2, 8, 2, 1, 4096, 48) == 0  # not a kernel head dim
-    # more query rows per K/V head never shrink the scratch
-    assert lib.fla_lazy_decode_workspace_size(1, 8, 1, 4, 1000, 64) >= lib.fla_lazy_decode_workspace_size(1, 8, 1, 1, 1000, 64)
+    # 8 rows per K/V head at D = 64: the 16-bit path keeps the scores (8 rows x 1024 keys,
+    # fp32) besides the per-chunk partials; 32 rows at D = 64 read K again instead
+    ws = lib.fla_lazy_decode_workspace_size(1, 8, 1, 1, 1000, 64)
+    assert ws % 256 == 0 and ws >= 8 * 1024 * 4
+    assert lib.fla_lazy_decode_workspace_size(1, 8, 1, 4, 1000, 64) % 256 == 0
 
 
 def test_pure_helpers():

@@ -15,23 +15,19 @@ from oracle.lazy import lazy_forward
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("H,Hkv", [(4, 4), (8, 2), (6, 1)])
-@pytest.mark.parametrize("Lq", [1, 3, 17])
-@pytest.mark.parametrize("varlen", [None, [700, 9]])
-@pytest.mark.parametrize("D", [32, 64, 128])
-def test_decode_vs_square_oracle(H, Hkv, Lq, varlen, D):
+def _decode_case(H, Hkv, Lq, varlen, D, dtype, tol):
     from adasplash import lazy_attention_triton
 
-    banner("lazy decode", H, Hkv, Lq, varlen, D)
+    banner("lazy decode", H, Hkv, Lq, varlen, D, dtype)
     B, Lk, W = 2, 777, 100
     G = H // Hkv
-    qf = rand((B, H, Lk, D), torch.float32, 1)
-    k = rand((B, Hkv, Lk, D), torch.float32, 2)
-    v = rand((B, Hkv, Lk, D), torch.float32, 3)
+    qf = rand((B, H, Lk, D), dtype, 1)
+    k = rand((B, Hkv, Lk, D), dtype, 2)
+    v = rand((B, Hkv, Lk, D), dtype, 3)
     bias = rand((H, W), torch.float32, 4) * 0.5
     tau = torch.linspace(-1.0, 0.3, H)
     lens = [Lk] * B if varlen is None else varlen
-    q = torch.zeros(B, H, Lq, D)
+    q = torch.zeros(B, H, Lq, D, dtype=dtype)
     for b in range(B):
         for i in range(Lq):
             p = lens[b] - Lq + i
@@ -49,7 +45,26 @@ def test_decode_vs_square_oracle(H, Hkv, Lq, varlen, D):
     with torch.no_grad():
         out = lazy_attention_triton(q.to(DEV), k.to(DEV), v.to(DEV), bias.to(DEV), tau.to(DEV), window_size=W, varlen=vl)
     assert out.shape == (B, H, Lq, D)
-    assert_close(to_np(out), ref, 1e-5, "decode out")
+    assert_close(to_np(out), ref, tol, "decode out")
+
+
+@pytest.mark.parametrize("H,Hkv", [(4, 4), (8, 2), (6, 1)])
+@pytest.mark.parametrize("Lq", [1, 3, 17])
+@pytest.mark.parametrize("varlen", [None, [700, 9]])
+@pytest.mark.parametrize("D", [32, 64, 128])
+def test_decode_vs_square_oracle(H, Hkv, Lq, varlen, D):
+    _decode_case(H, Hkv, Lq, varlen, D, torch.float32, 1e-5)
+
+
+# 16-bit inputs with two or more query rows per K/V head take the matrix-core kernels (rows in
+# groups of 32: G * Lq = 102 rows spans four groups, the last one partial).
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("H,Hkv", [(4, 4), (8, 2), (6, 1)])
+@pytest.mark.parametrize("Lq", [1, 3, 17])
+@pytest.mark.parametrize("varlen", [None, [700, 9]])
+@pytest.mark.parametrize("D", [32, 128])
+def test_decode_lowp_vs_square_oracle(dtype, H, Hkv, Lq, varlen, D):
+    _decode_case(H, Hkv, Lq, varlen, D, dtype, 2e-2)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
