@@ -117,7 +117,9 @@ int fla_lazy_bwd(const fla_tensor4_t* q, const fla_tensor4_t* k, const fla_tenso
                  const int32_t* varlen, float* dbias, float* dtau, void* workspace, size_t workspace_bytes, int B,
                  int H, int Hkv, int L, int D, int dtype, float scale, void* stream);
 
-/* Bytes of caller-provided scratch for fla_lazy_decode_fwd (0 for invalid sizes). */
+/* Bytes of caller-provided scratch for fla_lazy_decode_fwd (0 for invalid sizes): per key chunk
+ * partials and, for 16-bit inputs with fewer than D/4 query rows per K/V head, an fp32 cache of
+ * the scores (rows x Lk).  The size does not depend on the dtype.  256-byte aligned. */
 size_t fla_lazy_decode_workspace_size(int B, int H, int Hkv, int Lq, int Lk, int D);
 
 /* Lazy attention over a KV cache (inference forward; decode and chunked prefill).  q, out are
