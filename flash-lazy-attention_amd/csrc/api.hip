@@ -6,6 +6,10 @@
 #include "args.h"
 #include "flashlazy_internal.h"
 
+#ifndef FLA_FOLD_VALUE
+#define FLA_FOLD_VALUE cu_count()
+#endif
+
 using namespace fla;
 
 namespace {
@@ -55,6 +59,21 @@ bool good_common(int B, int H, int L, int D, int dtype) {
     case FLA_BF16 * 1000 + 128: e = LAUNCH<BF16, 128>(ARGS, ##__VA_ARGS__); break; \
     default: return FLA_EUNSUPPORTED;                                             \
   }
+
+namespace {
+// Compute units of the current device (cached per device; 0 if the query fails).
+int cu_count() {
+  static int cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+}  // namespace
 
 extern "C" const char* fla_version(void) { return "flashlazy-gfx950 0.1.0"; }
 
@@ -180,6 +199,7 @@ extern "C" int fla_lazy_fwd(const fla_tensor4_t* q, const fla_tensor4_t* k, cons
   a.L = L;
   a.W = window;
   a.nQT = (L + 127) / 128;
+  a.fold = FLA_FOLD_VALUE;
   a.scale = scale;
   hipStream_t s = (hipStream_t)stream;
   hipError_t e;
@@ -222,6 +242,7 @@ extern "C" int fla_lazy_bwd(const fla_tensor4_t* q, const fla_tensor4_t* k, cons
   a.L = L;
   a.W = window;
   a.nQT = (L + 127) / 128;
+  a.fold = FLA_FOLD_VALUE;
   a.scale = scale;
   const size_t parts = (size_t)B * H * a.nQT;
   auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };

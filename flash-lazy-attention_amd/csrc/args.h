@@ -48,6 +48,7 @@ struct LazyArgs {
   int MW;
   int B, H, L, W, nQT;
   int G;                   // query heads per K/V head
+  int fold;                // workgroups per dispatch round (compute units); 0: plain order
   float scale;
 };
 
