@@ -152,23 +152,47 @@ def rope(x, base=10000.0):
     return (xf * cos + rot * sin).to(x.dtype)
 
 
-def bench_configs(dev, steps, warmup):
-    """The other BASELINE.json configs, each timed with HIP events on the launch stream."""
+def bench_configs(dev, steps, warmup, only=None):
+    """The other BASELINE.json configs, each timed with HIP events on the launch stream.
+    only: run one section ("cfg2", "cfg4", "lazy", "decode") -- for profiling runs."""
     from adasplash import adasplash, adasplash_no_block_mask, lazy_attention_triton
 
     res = {}
     g = torch.Generator(device="cpu").manual_seed(0)
+    want = lambda name: only is None or only == name
 
     def rnd(*shape, scale=1.0):
         return (torch.randn(*shape, generator=g) * scale).to(device=dev, dtype=torch.bfloat16)
 
+    if want("cfg2"):
+        res.update(_bench_cfg2(rnd, steps, warmup))
+    if want("cfg4"):
+        res.update(_bench_cfg4(rnd, steps, warmup))
+    if want("lazy"):
+        res.update(_bench_lazy(rnd, g, dev, steps, warmup))
+    if want("decode"):
+        res.update(_bench_decode(rnd, dev, steps, warmup))
+    return res
+
+
+def _bench_cfg2(rnd, steps, warmup):
+    from adasplash import adasplash_no_block_mask
+
+    res = {}
     # configs[1]: adasplash_no_block_mask forward, non-causal, [4, 12, 1024, 64]
     q, k, v = rnd(4, 12, 1024, 64), rnd(4, 12, 1024, 64), rnd(4, 12, 1024, 64)
     with torch.no_grad():
         ms = time_region(lambda: adasplash_no_block_mask(q, k, v, alpha=1.5, niter=10, is_causal=False), steps, warmup)
     res["cfg2_nomask_fwd_ms"] = ms
     res["cfg2_nomask_fwd_TFLOPs"] = 4.0 * 4 * 12 * 1024 * 1024 * 64 / (ms * 1e-3) / 1e12
+    return res
 
+
+def _bench_cfg4(rnd, steps, warmup):
+    from adasplash import adasplash
+
+    res = {}
+    dev = torch.device("cuda", 0)
     # configs[3]: varlen, 8 sequences with lengths U[512, 8192] padded to 8192, H=12
     lens = torch.randint(512, 8193, (8,), generator=torch.Generator().manual_seed(0))
     B, H, L, D = 8, 12, 8192, 64
@@ -187,8 +211,13 @@ def bench_configs(dev, steps, warmup):
         tag = "causal" if causal else "bidir"
         res[f"cfg4_varlen_{tag}_ms"] = ms
         res[f"cfg4_varlen_{tag}_TFLOPs"] = flops / (ms * 1e-3) / 1e12
-    del q, k, v, do, qr, kr, vr
+    return res
 
+
+def _bench_lazy(rnd, g, dev, steps, warmup):
+    from adasplash import lazy_attention_triton
+
+    res = {}
     # lazy attention fwd+bwd, [2, 8, 4096, 64], RoPE pre-applied, bias [8, 512], tau = -1
     B, H, L, D, W = 2, 8, 4096, 64, 512
     q, k = rope(rnd(B, H, L, D)), rope(rnd(B, H, L, D))
@@ -225,7 +254,14 @@ def bench_configs(dev, steps, warmup):
                 lambda: lazy_attention_triton(q, k, v, bias, tt, window_size=W), steps, warmup)
             res[f"cfg5_lazy_tau{int(tv)}_fwd_ms_blocksparse"] = time_region(
                 lambda: lazy_attention_triton(q, k, v, bias, tt, window_size=W, return_mask=True), steps, warmup)
-    del q, k, v, do, qr, kr, vr
+    return res
+
+
+def _bench_decode(rnd, dev, steps, warmup):
+    from adasplash import lazy_attention_triton
+
+    res = {}
+    D, W = 64, 512
     # KV-cache decode (one new token, GQA 32 query heads over 8 K/V heads, 8192 cached keys)
     Bd, Hd, Hkv, Lk = 8, 32, 8, 8192
     qd, kd, vd = rnd(Bd, Hd, 1, D), rnd(Bd, Hkv, Lk, D), rnd(Bd, Hkv, Lk, D)
@@ -299,6 +335,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline step only (for profiling runs)")
+    ap.add_argument("--only", choices=["cfg2", "cfg4", "lazy", "decode"],
+                    help="time one of the other configs only and print its figures (for profiling runs)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only copy a 256 MiB buffer 3 times (calibrates the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
@@ -317,6 +355,9 @@ def main():
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     torch.cuda.synchronize()
+    if args.only:
+        print(json.dumps({k_: round(v_, 4) for k_, v_ in bench_configs(dev, args.steps, args.warmup, args.only).items()}))
+        return
     res, shape = bench_attention(args, dev)
     B, H, L, D = shape
     fwd, bwd = dense_flops(B, H, L, D)
