@@ -54,9 +54,10 @@ def test_backward_vs_reference_fp32(tauval, shape):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_lowp_forward_backward(dtype):
-    banner("lazy lowp", dtype)
-    B, H, L, D, W = 2, 2, 384, 64, 96
+@pytest.mark.parametrize("D", [32, 64, 128])
+def test_lowp_forward_backward(dtype, D):
+    banner("lazy lowp", dtype, D)
+    B, H, L, W = 2, 2, 384, 96
     q, k, v, bias, tau = _case(B, H, L, D, W, dtype, seed=9)
     bias = bias * 0.5
     do = rand((B, H, L, D), dtype, 10)
