@@ -84,6 +84,9 @@ def reference_attention(q, k, v, alpha=1.5, varlen=None, is_causal=False, method
             s = q[b, h] @ k[b, h].T / math.sqrt(D)
             s = np.where(valid[b], s, -np.inf)
             p, tau = entmax_rows(s, alpha, method)
+            # rows past the length hold no probability (a length-0 sequence has no finite
+            # score at all, where entmax of an all -inf row is undefined)
+            p = np.where(rowv[b][:, None], p, 0.0)
             o = p @ v[b, h]
             o[~rowv[b]] = 0.0
             out[b, h] = o
@@ -113,10 +116,12 @@ def reference_attention_backward(q, k, v, do, alpha=1.5, varlen=None, is_causal=
             s = q[b, h] @ k[b, h].T * sc
             s = np.where(valid[b], s, -np.inf)
             p, _ = entmax_rows(s, alpha, method)
+            p = np.where(rowv[b][:, None], p, 0.0)
             g = np.where(rowv[b][:, None], do[b, h], 0.0)
             dP = g @ v[b, h].T
             u = np.where(p > 0, np.where(p > 0, p, 1.0) ** (2.0 - alpha), 0.0)
-            delta = (u * dP).sum(-1, keepdims=True) / u.sum(-1, keepdims=True)
+            den = u.sum(-1, keepdims=True)  # 0 only on rows past the length
+            delta = np.where(den > 0, (u * dP).sum(-1, keepdims=True) / np.where(den > 0, den, 1.0), 0.0)
             dS = u * (dP - delta)
             dq[b, h] = dS @ k[b, h] * sc
             dk[b, h] = dS.T @ q[b, h] * sc

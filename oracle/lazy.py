@@ -48,6 +48,17 @@ def _scores(q, k, bias, window, varlen, b, h, L):
     return s, valid, keyok, d, inwin
 
 
+def _softmax_rows(sm, ok):
+    """p = exp(sm - LSE) per row and LSE; a row with no visible key (a length-0 sequence) has
+    p = 0 and LSE = -inf."""
+    mx = sm.max(-1, keepdims=True)
+    mx = np.where(np.isfinite(mx), mx, 0.0)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        lse = mx + np.log(np.exp(sm - mx).sum(-1, keepdims=True))
+        p = np.where(ok & np.isfinite(lse), np.exp(sm - lse), 0.0)
+    return p, lse
+
+
 def lazy_forward(q, k, v, bias, tau, window=None, varlen=None, return_aux=False):
     q, k, v = (np.asarray(t, dtype=np.float64) for t in (q, k, v))
     bias = np.asarray(bias, dtype=np.float64)
@@ -62,9 +73,7 @@ def lazy_forward(q, k, v, bias, tau, window=None, varlen=None, return_aux=False)
         for h in range(H):
             s, valid, keyok, _, _ = _scores(q, k, bias, window, varlen, b, h, L)
             sm = np.where(valid & keyok, s, -np.inf)
-            mx = sm.max(-1, keepdims=True)
-            lse = mx + np.log(np.exp(sm - mx).sum(-1, keepdims=True))
-            p = np.exp(sm - lse)
+            p, lse = _softmax_rows(sm, valid & keyok)
             ti = tau[h] / np.arange(1, L + 1)[:, None]
             e = np.where(valid, np.maximum(p + ti, 0.0), 0.0)
             e = np.where(keyok, e, 0.0)
@@ -96,9 +105,7 @@ def lazy_backward(q, k, v, bias, tau, do, window=None, varlen=None):
         for h in range(H):
             s, valid, keyok, d, inwin = _scores(q, k, bias, window, varlen, b, h, L)
             sm = np.where(valid & keyok, s, -np.inf)
-            mx = sm.max(-1, keepdims=True)
-            lse = mx + np.log(np.exp(sm - mx).sum(-1, keepdims=True))
-            p = np.exp(sm - lse)
+            p, lse = _softmax_rows(sm, valid & keyok)
             inv_i = 1.0 / np.arange(1, L + 1)[:, None]
             m = (p + tau[h] * inv_i > 0) & valid & keyok
             e = np.where(valid & keyok, np.maximum(p + tau[h] * inv_i, 0.0), 0.0)
