@@ -2,6 +2,7 @@
 // on dtype / head dim / alpha.  Nothing here allocates; all launches are asynchronous on
 // the caller's stream.
 #include <algorithm>
+#include <atomic>
 
 #include "args.h"
 #include "flashlazy_internal.h"
@@ -61,17 +62,18 @@ bool good_common(int B, int H, int L, int D, int dtype) {
   }
 
 namespace {
-// Compute units of the current device (cached per device; 0 if the query fails).
+// Compute units of the current device (cached per device; 0 if the query fails).  Concurrent
+// first calls may both query; they store the same value.
 int cu_count() {
-  static int cache[64];
+  static std::atomic<int> cache[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (cache[dev] == 0) {
-    int n = 0;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    cache[dev] = n;
+    cache[dev].store(n, std::memory_order_relaxed);
   }
-  return cache[dev];
+  return n;
 }
 }  // namespace
 
