@@ -94,17 +94,33 @@ __device__ __forceinline__ float pair_sum(float x) { return x + __shfl_xor(x, 32
 __device__ __forceinline__ float pair_max(float x) { return fmaxf(x, __shfl_xor(x, 32)); }
 __device__ __forceinline__ float pair_min(float x) { return fminf(x, __shfl_xor(x, 32)); }
 
-__device__ __forceinline__ float wave_sum(float x) {
-  for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m);
+// Whole-wave reductions, every lane gets the result.  Within a row of 16 lanes the four
+// exchange steps are DPP operand modifiers of the VALU op itself (quad permutations for lane
+// xor 1 and 2; once the 4 lanes of a quad agree, the half-row mirror pairs quad q with quad
+// q ^ 1 and the row mirror pairs the two halves of the row); the xor-16 and xor-32 steps cross
+// rows through the LDS crossbar.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+template <typename Op>
+__device__ __forceinline__ float wave_reduce(float x, Op op) {
+  x = op(x, dpp_f<0xB1>(x));   // quad_perm [1,0,3,2]: lane ^ 1
+  x = op(x, dpp_f<0x4E>(x));   // quad_perm [2,3,0,1]: lane ^ 2
+  x = op(x, dpp_f<0x141>(x));  // row_half_mirror: quad pairs within 8 lanes
+  x = op(x, dpp_f<0x140>(x));  // row_mirror: the two 8-lane halves of a row
+  x = op(x, __shfl_xor(x, 16));
+  x = op(x, __shfl_xor(x, 32));
   return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+  return wave_reduce(x, [](float a, float b) { return a + b; });
 }
 __device__ __forceinline__ float wave_max(float x) {
-  for (int m = 32; m >= 1; m >>= 1) x = fmaxf(x, __shfl_xor(x, m));
-  return x;
+  return wave_reduce(x, [](float a, float b) { return fmaxf(a, b); });
 }
 __device__ __forceinline__ float wave_min(float x) {
-  for (int m = 32; m >= 1; m >>= 1) x = fminf(x, __shfl_xor(x, m));
-  return x;
+  return wave_reduce(x, [](float a, float b) { return fminf(a, b); });
 }
 
 // t^beta and t^(beta-1) for t > 0.  MODE 1: alpha = 1.5 (beta = 2), MODE 2: alpha = 2
