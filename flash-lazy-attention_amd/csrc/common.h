@@ -229,6 +229,9 @@ __device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t o
   u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
+// s_waitcnt vmcnt(0): wait for every outstanding vector-memory load of this wave.
+__device__ __forceinline__ void vm_wait_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 // Bytes covering rows [0, nvalid) of a tile with row stride ld and D columns.
 template <typename T, int D>
 __device__ __forceinline__ uint32_t tile_bytes(int64_t ld, int nvalid) {
@@ -258,14 +261,14 @@ struct RowTile {
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(g, tile_bytes<T, D>(ld, min(nvalid, ROWS)));
 #pragma unroll
     for (int i = 0; i < PER; ++i)
-      if (tid + NT * i < NCH) r[i] = buf_load16(rs, off[i]);
+      if (NCH % NT == 0 || tid + NT * i < NCH) r[i] = buf_load16(rs, off[i]);
   }
   __device__ __forceinline__ void store(T* __restrict__ lds, int tid) const {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int c = tid + NT * i;
       const int row = c / CPR, col = (c % CPR) * EPV;
-      if (c < NCH) *reinterpret_cast<uint4*>(lds + row * LDR + col) = r[i];
+      if (NCH % NT == 0 || c < NCH) *reinterpret_cast<uint4*>(lds + row * LDR + col) = r[i];
     }
   }
 };
@@ -305,7 +308,7 @@ struct TransTile {
     const uint32_t step = (uint32_t)(ld * sizeof(T));
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-      if (tid + NT * i >= NU) continue;
+      if (NU % NT != 0 && tid + NT * i >= NU) continue;
       r0[i] = buf_load16(rs, off[i]);
       if constexpr (PAIR) r1[i] = buf_load16(rs, off[i] + step);
     }
@@ -314,7 +317,7 @@ struct TransTile {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int u = tid + NT * i;
-      if (u >= NU) continue;
+      if (NU % NT != 0 && u >= NU) continue;
       if constexpr (PAIR) {
         const int kp = u % (ROWS / 2), col = (u / (ROWS / 2)) * EPV;
         const int k = 2 * kp, pos = (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1);
