@@ -92,11 +92,18 @@ def t4(x):
 
 
 def ptr(x):
-    return None if x is None else ctypes.c_void_p(x.data_ptr())
+    # A plain int: ctypes converts it for c_void_p parameters without building a wrapper.
+    return None if x is None else x.data_ptr()
+
+
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
 def stream_of(x):
-    return ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)
+    """Handle of the current HIP stream of x's device (an int; cheaper than a Stream object)."""
+    if _raw_stream is not None:
+        return _raw_stream(x.get_device())
+    return torch.cuda.current_stream(x.device).cuda_stream
 
 
 def kernel_head_dim(D):
