@@ -91,7 +91,8 @@ int fla_adasplash_bwd(const fla_tensor4_t* q, const fla_tensor4_t* k, const fla_
  * with bias[h, i-j] added for 0 <= i-j < window.  Replaces `lazy_attention_triton`'s
  * forward (reference lazy_attention_triton.py:503-515, 543-583; kernels :9-174).
  *   bias fp32 [H, >= window] with row stride bias_ld; tau fp32 [H].
- *   lse [B, H, L] fp32 out (log-sum-exp of the scores, natural log).
+ *   lse [B, H, L] fp32 out: log-sum-exp of the scores in base-2 units, log2 sum_j 2^(s_ij log2 e)
+ *        (= natural-log LSE * log2 e), the form fla_lazy_bwd consumes; +inf on rows >= varlen.
  *   wdelta [B, H, L, D] fp32 out, optional (needed by the backward):
  *          sum_j 1[p_ij + tau/(i+1) > 0] p_ij v_j.
  *   block_mask [B, H, ceil(L/64), fla_adasplash_mask_words(L)] uint32 out, optional: bit c%32

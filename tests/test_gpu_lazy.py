@@ -192,3 +192,26 @@ def test_block_mask_with_autograd():
     for a, b, n in zip(*grads, ("dq", "dk", "dv", "dbias", "dtau")):
         # dbias / dtau sum per-tile partials built with LDS float atomics: equal up to order
         assert torch.equal(a, b) if n in ("dq", "dk", "dv") else torch.allclose(a, b, rtol=1e-5, atol=1e-6), n
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_tie_at_row_zero_consistent(dtype):
+    """tau = -1 puts row 0 exactly on the threshold (p = 1, p + tau/1 = 0).  Whichever side the
+    float32 rounding picks, the forward (wdelta, hence delta) and the backward must pick the same
+    one, and then dS of row 0 vanishes: dq row 0 = 0 on every head (regression: the backward
+    re-derived p from a natural-log LSE and could disagree with the forward)."""
+    banner("lazy row-0 tie", dtype)
+    B, H, L, D, W = 2, 8, 200, 64, 64
+    q, k, v, bias, tau = _case(B, H, L, D, W, dtype, seed=21, tau=-1.0)
+    bias = bias * 0.5
+    do = rand((B, H, L, D), dtype, 22)
+    ts = [t.to(DEV).requires_grad_(True) for t in (q, k, v, bias, tau)]
+    out = _op()(*ts)
+    out.backward(do.to(DEV))
+    # the row's one key gets p = 1 exactly, so e = relu(1 - 1) = 0 exactly, as in exact arithmetic
+    assert (out[:, :, 0] == 0).all()
+    assert ts[0].grad[:, :, 0].abs().max().item() < 1e-4
+    ref = lazy_backward(to_np(q), to_np(k), to_np(v), to_np(bias), to_np(tau), to_np(do), W)
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    for got, r, n in zip([t.grad for t in ts], ref, ["dq", "dk", "dv", "dbias", "dtau"]):
+        assert_close(to_np(got), r, tol * max(1.0, np.abs(r).max() / 4), n)
