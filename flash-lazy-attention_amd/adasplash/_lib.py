@@ -53,6 +53,10 @@ SIGNATURES = {
         [_T4, _T4, _T4, _T4, _P, _I64, _P, _I, _P, _P, ctypes.c_size_t, _I, _I, _I, _I, _I, _I, _I, _F, _P],
         _I,
     ),
+    "fla_lazy_decode_fwd_static": (
+        [_T4, _T4, _T4, _T4, _P, _I64, _P, _I, _P, _I, _I, _I, _I, _I, _I, _I, _F, _P],
+        _I,
+    ),
     "fla_lazy_bwd": (
         [_T4, _T4, _T4, _T4, _T4, _T4, _T4, _P, _I64, _P, _I, _P, _P, _P, _P, _P, _P, ctypes.c_size_t,
          _I, _I, _I, _I, _I, _I, _F, _P],

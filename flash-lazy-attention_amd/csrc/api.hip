@@ -3,6 +3,7 @@
 // the caller's stream.
 #include <algorithm>
 #include <atomic>
+#include <mutex>
 
 #include "args.h"
 #include "flashlazy_internal.h"
@@ -315,10 +316,17 @@ extern "C" size_t fla_lazy_decode_workspace_size(int B, int H, int Hkv, int Lq, 
   return std::max(p.bytes(), pm.bytes());
 }
 
-extern "C" int fla_lazy_decode_fwd(const fla_tensor4_t* q, const fla_tensor4_t* k, const fla_tensor4_t* v,
-                                   const fla_tensor4_t* out, const float* bias, int64_t bias_ld, const float* tau,
-                                   int window, const int32_t* varlen, void* workspace, size_t workspace_bytes, int B,
-                                   int H, int Hkv, int Lq, int Lk, int D, int dtype, float scale, void* stream) {
+// Static scratch of fla_lazy_decode_fwd_static: one copy per GPU, held until the process ends.
+// Host code never uses the name `scratch` as an address (on the host it is only a stand-in
+// for the device symbol): the device address comes from hipGetSymbolAddress, once per device.
+static __device__ __align__(256) char scratch[FLA_STATIC_SCRATCH_BYTES];
+
+namespace {
+
+int lazy_decode(const fla_tensor4_t* q, const fla_tensor4_t* k, const fla_tensor4_t* v, const fla_tensor4_t* out,
+                const float* bias, int64_t bias_ld, const float* tau, int window, const int32_t* varlen,
+                void* workspace, size_t workspace_bytes, int B, int H, int Hkv, int Lq, int Lk, int D, int dtype,
+                float scale, void* stream) {
   if (dtype != FLA_F32 && dtype != FLA_F16 && dtype != FLA_BF16) return FLA_EUNSUPPORTED;
   DecPlan p;
   if (!dec_plan(B, H, Hkv, Lq, Lk, D, dtype != FLA_F32, p)) return FLA_EINVAL;
@@ -355,4 +363,51 @@ extern "C" int fla_lazy_decode_fwd(const fla_tensor4_t* q, const fla_tensor4_t* 
   hipError_t e;
   FLA_DISPATCH(lazy_decode_launch, a, s)
   return (int)e;
+}
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];  // guarded by g_scratch_mu
+
+// Device address of the current device's scratch (resolved on the first call per device).
+int static_scratch(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return FLA_EUNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (!p) return (int)hipErrorInvalidSymbol;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
+}  // namespace
+
+extern "C" int fla_lazy_decode_fwd(const fla_tensor4_t* q, const fla_tensor4_t* k, const fla_tensor4_t* v,
+                                   const fla_tensor4_t* out, const float* bias, int64_t bias_ld, const float* tau,
+                                   int window, const int32_t* varlen, void* workspace, size_t workspace_bytes, int B,
+                                   int H, int Hkv, int Lq, int Lk, int D, int dtype, float scale, void* stream) {
+  return lazy_decode(q, k, v, out, bias, bias_ld, tau, window, varlen, workspace, workspace_bytes, B, H, Hkv, Lq, Lk,
+                     D, dtype, scale, stream);
+}
+
+extern "C" int fla_lazy_decode_fwd_static(const fla_tensor4_t* q, const fla_tensor4_t* k, const fla_tensor4_t* v,
+                                          const fla_tensor4_t* out, const float* bias, int64_t bias_ld,
+                                          const float* tau, int window, const int32_t* varlen, int B, int H, int Hkv,
+                                          int Lq, int Lk, int D, int dtype, float scale, void* stream) {
+  const size_t need = fla_lazy_decode_workspace_size(B, H, Hkv, Lq, Lk, D);
+  if (need == 0) return FLA_EINVAL;
+  if (need > FLA_STATIC_SCRATCH_BYTES) return FLA_EWORKSPACE;
+  void* ws = nullptr;
+  const int rc = static_scratch(&ws);
+  if (rc != 0) return rc;
+  // Every scratch byte the kernels read is written earlier in the same call: nothing to clear.
+  return lazy_decode(q, k, v, out, bias, bias_ld, tau, window, varlen, ws, FLA_STATIC_SCRATCH_BYTES, B, H, Hkv, Lq,
+                     Lk, D, dtype, scale, stream);
 }

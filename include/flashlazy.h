@@ -135,6 +135,22 @@ int fla_lazy_decode_fwd(const fla_tensor4_t* q, const fla_tensor4_t* k, const fl
                         const int32_t* varlen, void* workspace, size_t workspace_bytes, int B, int H, int Hkv, int Lq,
                         int Lk, int D, int dtype, float scale, void* stream);
 
+/* Bytes of the static per-GPU scratch behind fla_lazy_decode_fwd_static (64 MiB). */
+#define FLA_STATIC_SCRATCH_BYTES ((size_t)64 << 20)
+
+/* fla_lazy_decode_fwd without a workspace argument.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture, serving loops or
+ * harnesses that forbid hipMalloc).  It calls no allocator; its scratch is a static device array
+ * of FLA_STATIC_SCRATCH_BYTES that every GPU the library runs on holds until the process ends.
+ * Returns FLA_EWORKSPACE when fla_lazy_decode_workspace_size(B, H, Hkv, Lq, Lk, D) exceeds that
+ * size (use fla_lazy_decode_fwd there).  All calls on one GPU share its scratch: calls that
+ * overlap in time on one GPU (e.g. on two streams) race and must be serialised by the caller.
+ * Results are those of fla_lazy_decode_fwd. */
+int fla_lazy_decode_fwd_static(const fla_tensor4_t* q, const fla_tensor4_t* k, const fla_tensor4_t* v,
+                               const fla_tensor4_t* out, const float* bias, int64_t bias_ld, const float* tau,
+                               int window, const int32_t* varlen, int B, int H, int Hkv, int Lq, int Lk, int D,
+                               int dtype, float scale, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
