@@ -167,9 +167,11 @@ extern "C" size_t fla_lazy_bwd_workspace_size(int B, int H, int L, int window) {
   if (B <= 0 || H <= 0 || L <= 0 || window <= 0) return 0;
   const size_t nqt = (size_t)(L + 127) / 128;
   const size_t parts = (size_t)B * H * nqt;
-  // dbias partials, dtau partials, delta [B, H, L]; each region 256-byte aligned.
+  // dbias partials, dtau partials, delta [B, H, L], per-wave dbias partials of distances
+  // >= LZ_SB; each region 256-byte aligned.
   auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
-  return up(parts * (size_t)window * 4) + up(parts * 4) + up((size_t)B * H * L * 4);
+  const size_t nfar = window > LZ_SB ? (size_t)(window - LZ_SB) : 0;
+  return up(parts * (size_t)window * 4) + up(parts * 4) + up((size_t)B * H * L * 4) + up(parts * 4 * nfar * 4);
 }
 
 extern "C" int fla_lazy_fwd(const fla_tensor4_t* q, const fla_tensor4_t* k, const fla_tensor4_t* v,
@@ -253,6 +255,7 @@ extern "C" int fla_lazy_bwd(const fla_tensor4_t* q, const fla_tensor4_t* k, cons
   a.dbias_part = (float*)ws;
   a.dtau_part = (float*)(ws + up(parts * (size_t)window * 4));
   a.delta = (float*)(ws + up(parts * (size_t)window * 4) + up(parts * 4));
+  a.dbias_far = (float*)(ws + up(parts * (size_t)window * 4) + up(parts * 4) + up((size_t)B * H * L * 4));
   a.dbias = dbias;
   a.dtau = dtau;
   hipStream_t s = (hipStream_t)stream;

@@ -30,6 +30,9 @@ struct AdaBwdArgs {
   int causal;
 };
 
+// Lazy bias entries staged in LDS per workgroup; distances >= LZ_SB read global memory.
+static constexpr int LZ_SB = 1024;
+
 struct LazyArgs {
   Tensor4 q, k, v, o, dout, dq, dk, dv;
   const float* bias;       // fp32 [H, bias_ld]
@@ -40,6 +43,7 @@ struct LazyArgs {
   float* delta;            // [B, H, L] scratch (backward)
   const int32_t* varlen;
   float* dbias_part;       // [B*H*nQT, window] per-tile partials (backward, optional)
+  float* dbias_far;        // [B*H*nQT*4, window - LZ_SB] per-wave partials of distances >= LZ_SB
   float* dtau_part;        // [B*H*nQT]
   float* dbias;            // [H, window]
   float* dtau;             // [H]
