@@ -104,6 +104,11 @@ def bench_attention(args, dev):
             L_.ptr(mask), None, L_.ptr(delta), B, H, H, L, D, L_.FLA_BF16, 1.5, 1, scale, L_.stream_of(q))
         L_.check(rc, "bwd")
 
+    # slice (0, 0) of one step's results, for the CPU leg's check
+    qr_, kr_, vr_ = (t.clone().requires_grad_(True) for t in (q, k, v))
+    o_ = adasplash(qr_, kr_, vr_, alpha=1.5, niter=10, is_causal=True)
+    o_.backward(do)
+    res["_slice"] = tuple(t.detach().cpu() for t in (q, k, v, do, o_, qr_.grad))
     res["fwd_kernel_ms"] = time_region(fwd_call, args.steps, args.warmup)
     res["bwd_calls_ms"] = time_region(bwd_call, args.steps, args.warmup)
     dens = mask.view(torch.int32).cpu().numpy().view(np.uint32)
@@ -278,8 +283,23 @@ def _bench_lazy(rnd, g, dev, steps, warmup):
     with torch.no_grad():
         msf = time_region(lambda: lazy_attention_triton(q, k, v, bias, tau, window_size=W), steps, warmup)
     res["cfg5_lazy_fwd_ms"] = msf
-    lvl = torch.randint(L // 8, L + 1, (B,), generator=torch.Generator().manual_seed(1)).to(dev)
-    res["cfg5_lazy_varlen_ms"] = time_region(run_lazy(lvl.to(torch.int32)), steps, warmup)
+    # varlen variant: 4 sequences of seeded lengths in [512, 4096] padded to L
+    B4 = 4
+    lens = torch.randint(512, L + 1, (B4,), generator=torch.Generator().manual_seed(1))
+    q4, k4 = rope(rnd(B4, H, L, D)), rope(rnd(B4, H, L, D))
+    v4, do4 = rnd(B4, H, L, D), rnd(B4, H, L, D)
+    q4r, k4r, v4r = (t.clone().requires_grad_(True) for t in (q4, k4, v4))
+    vl4 = lens.to(dev, torch.int32)
+
+    def run_var():
+        for t in (q4r, k4r, v4r, bias, tau):
+            t.grad = None
+        lazy_attention_triton(q4r, k4r, v4r, bias, tau, window_size=W, varlen=vl4).backward(do4)
+
+    msv = time_region(run_var, steps, warmup)
+    s2 = float((lens.double() ** 2).sum())
+    res["cfg5_lazy_varlen4_ms"] = msv
+    res["cfg5_lazy_varlen4_TFLOPs"] = 7.0 * H * D * s2 / (msv * 1e-3) / 1e12
     # block-sparse lazy forward (return_mask: 64x64 blocks with relu(p + tau/i) > 0, empty ones skipped)
     from adasplash import get_sparsity_stats
 
@@ -311,58 +331,47 @@ def _bench_decode(rnd, dev, steps, warmup):
     return res
 
 
-def cpu_baseline(shape, budget_s=12.0):
-    """The CPU oracle (numpy float64 bisection entmax attention, forward + backward) on a
-    bounded row sample of slice (b=0, h=0) at L=8192, extrapolated to the full step by the
-    number of (query, key) pairs."""
-    from oracle.adasplash import entmax_rows
+def cpu_baseline(shape, gpu_res, budget_s=12.0):
+    """The reference's PyTorch CPU path (oracle.torch_cpu: float32 torch, entmax bisection with
+    the entmax package's 50 iterations, forward + backward) on all host cores, over whole (b, h)
+    slices of the same inputs, in blocks of 128 query rows, until about ``budget_s`` seconds;
+    extrapolated to the full step by the number of causal (query, key) pairs.  The GPU's out
+    and dq of the same rows are checked against it on the way."""
+    from oracle.torch_cpu import attention_rows
 
     B, H, L, D = shape
-    rng = np.random.default_rng(0)
-    q, k, v, do = (rng.standard_normal((L, D)).astype(np.float32).astype(np.float64) for _ in range(4))
-    sc = 1.0 / math.sqrt(D)
-
-    def run(rows):
-        t0 = time.perf_counter()
-        pairs = 0
-        for i in rows:
-            n = i + 1
-            s = (k[:n] @ q[i]) * sc
-            p, _ = entmax_rows(s[None, :], 1.5, method="bisect", n_iter=50)
-            p = p[0]
-            _o = p @ v[:n]
-            dP = v[:n] @ do[i]
-            u = np.sqrt(p)
-            dS = u * (dP - (u * dP).sum() / u.sum())
-            _dq = dS @ k[:n] * sc
-            _dk = np.outer(dS, q[i]) * sc
-            _dv = np.outer(p, do[i])
-            pairs += n
-        return time.perf_counter() - t0, pairs
-
-    from threadpoolctl import threadpool_limits
-
-    limiter = threadpool_limits(1)
-    nrows = 16
-    while True:
-        rows = np.linspace(0, L - 1, nrows).astype(int)
-        t, pairs = run(rows)
-        if t >= 0.5 * budget_s or nrows >= L:
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or os.cpu_count()
+    torch.set_num_threads(threads)
+    q, k, v, do, g_out, g_dq = gpu_res
+    t_cpu, pairs, nsl = 0.0, 0, 0
+    err_out, err_dq = 0.0, 0.0
+    for bh in range(B * H):
+        b, h = divmod(bh, H)
+        x = [t[b, h].float() for t in (q, k, v, do)]
+        for r0 in range(0, L, 128):
+            rows = np.arange(r0, r0 + 128)
+            t0 = time.perf_counter()
+            out, dq, _dk, _dv = attention_rows(*x, rows, 1.5, True)
+            t_cpu += time.perf_counter() - t0
+            pairs += int((rows + 1).sum())
+            err_out = max(err_out, float((out - g_out[b, h, r0:r0 + 128].float()).abs().max()))
+            err_dq = max(err_dq, float((dq - g_dq[b, h, r0:r0 + 128].float()).abs().max()))
+        nsl += 1
+        if t_cpu >= budget_s:
             break
-        nrows = int(min(L, max(2 * nrows, nrows * budget_s / max(t, 1e-3))))
-    limiter.unregister()
     total_pairs = B * H * L * (L + 1) / 2
-    step_s = t * total_pairs / pairs
+    step_s = t_cpu * total_pairs / pairs
     fwd, bwd = dense_flops(B, H, L, D)
     return {
         "value": float((fwd + bwd) / step_s / 1e12),
         "unit": "TFLOP/s",
-        "cores": 1,
+        "cores": threads,
         "kind": "port",
-        "sample": f"{nrows} causal query rows of one (b,h) slice at L=8192 (numpy float64 bisection entmax, "
-                  f"50 iters, fwd+bwd), {t:.1f}s, extrapolated x{total_pairs / pairs:.0f} by (query,key) pairs "
-                  f"to {step_s:.0f}s per step",
+        "sample": f"{nsl} of {B * H} (b,h) slices at L=8192, causal, in blocks of 128 query rows (float32 torch, "
+                  f"{threads} threads, entmax bisection 50 iters, fwd+bwd), {t_cpu:.1f}s, extrapolated "
+                  f"x{total_pairs / pairs:.1f} by (query,key) pairs to {step_s:.0f}s per step",
         "ms_per_step": float(step_s * 1e3),
+        "gpu_check_max_abs_err": {"out": err_out, "dq": err_dq},
     }
 
 
@@ -397,6 +406,7 @@ def main():
         print(json.dumps({k_: round(v_, 4) for k_, v_ in bench_configs(dev, args.steps, args.warmup, args.only).items()}))
         return
     res, shape = bench_attention(args, dev)
+    gpu_slice = res.pop("_slice")
     B, H, L, D = shape
     fwd, bwd = dense_flops(B, H, L, D)
     tflops = (fwd + bwd) / (res["ms_a15"] * 1e-3) / 1e12
@@ -437,7 +447,7 @@ def main():
         "extra": {k_: (round(v_, 4) if isinstance(v_, float) else v_) for k_, v_ in extra.items()},
     }
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(shape)
+        line["cpu_baseline"] = cpu_baseline(shape, gpu_slice)
     print(json.dumps(line), flush=True)
 
 

@@ -94,3 +94,28 @@ def test_unit_round_bounds_bf16_operand_rounding():
     assert (np.abs(bf(r["p"]) @ v - r["out"]) <= r["out_round"] + 1e-12).all()
     assert (np.abs(bf(r["ds"]) @ k / 8 - r["dq"]) <= r["dq_round"] + 1e-12).all()
     assert r["dq_round"].max() > 0
+
+
+@pytest.mark.parametrize("alpha", [1.5, 2.0])
+def test_torch_cpu_path_matches_oracle(alpha):
+    """oracle.torch_cpu (the float32 torch path bench.py times as the CPU baseline) against the
+    float64 oracle: rows 0..L-1 in two blocks, causal."""
+    import torch
+
+    from oracle.torch_cpu import attention_rows
+
+    rng = np.random.default_rng(9)
+    L, D = 200, 32
+    q, k, v, do = (rng.standard_normal((1, 1, L, D)) for _ in range(4))
+    out = reference_attention(q, k, v, alpha, None, True)
+    dq, dk, dv = reference_attention_backward(q, k, v, do, alpha, None, True)
+    t = [torch.tensor(a[0, 0], dtype=torch.float32) for a in (q, k, v, do)]
+    acc = [np.zeros((L, D)) for _ in range(4)]
+    for rows in (np.arange(0, 120), np.arange(120, L)):
+        o, gq, gk, gv = attention_rows(*t, rows, alpha)
+        acc[0][rows] = o.numpy()
+        acc[1][rows] = gq.numpy()
+        acc[2] += gk.numpy()
+        acc[3] += gv.numpy()
+    for got, ref in zip(acc, (out[0, 0], dq[0, 0], dk[0, 0], dv[0, 0])):
+        np.testing.assert_allclose(got, ref, atol=2e-4)
