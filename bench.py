@@ -33,7 +33,7 @@ PEAK_HBM_GBPS = 8000.0
 # HBM bytes per launch of ada_fwd_kernel at the headline config, from two rocprofv3 --pmc
 # passes (FETCH_SIZE x2.000, WRITE_SIZE x1.000 after calibration on a plain 256 MiB copy);
 # source: profiles/adasplash_causal_L8192_a15_traffic.txt.
-FWD_TRAFFIC_BYTES = (140828 * 2.0 + 99387 * 1.0) * 1024
+FWD_TRAFFIC_BYTES = (157870 * 2.0 + 99385 * 1.0) * 1024
 
 
 def dense_flops(B, H, L, D, causal=True):
@@ -45,9 +45,18 @@ def _events():
     return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
 
-def time_region(fn, steps, warmup):
-    for _ in range(warmup):
+def time_region(fn, steps, warmup, min_warm_s=0.2):
+    """Mean ms per call of fn over `steps` calls, timed with events on the current stream.
+    The warm-up runs at least `warmup` calls and at least `min_warm_s` seconds: after the GPU
+    has idled (host work between regions), its clock takes ~20-30 ms of work to return to
+    steady state, and calls in that window run up to ~25% slow."""
+    t_end = time.perf_counter() + min_warm_s
+    n = 0
+    while n < warmup or time.perf_counter() < t_end:
         fn()
+        n += 1
+        if n % 8 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
     s, e = _events()
     s.record()
@@ -79,12 +88,6 @@ def bench_attention(args, dev):
         return run
 
     res = {}
-    # bring the GPU to its steady clock before the first timed region (about half a second of
-    # steps; the first measurement otherwise reads up to ~15% slow)
-    t_end = time.perf_counter() + 0.5
-    while time.perf_counter() < t_end:
-        step(adasplash, 1.5)()
-    torch.cuda.synchronize()
     res["ms_a15"] = time_region(step(adasplash, 1.5), args.steps, args.warmup)
     if not args.quick:
         res["ms_a20"] = time_region(step(adasplash, 2.0), args.steps, args.warmup)
