@@ -164,8 +164,15 @@ def prep_varlen(varlen, B, device):
     return vl.to(torch.int32).contiguous()
 
 
+_BITSEL = {}
+
+
 def unpack_block_mask(words, ncols):
     """int32 [..., R, MW] bit rows (bit c%32 of word c/32 = column c) -> bool [..., R, ncols]."""
-    bits = torch.arange(32, device=words.device, dtype=torch.int32)
-    m = (words.unsqueeze(-1) >> bits) & 1
-    return m.reshape(*words.shape[:-1], -1)[..., :ncols].bool()
+    sel = _BITSEL.get(words.device)
+    if sel is None:  # 1 << c for c = 0..31 as int32 (bit 31 is the sign bit), made once per device
+        sel = torch.tensor([1 << c if c < 31 else -(1 << 31) for c in range(32)], dtype=torch.int32,
+                           device=words.device)
+        _BITSEL[words.device] = sel
+    m = (words.unsqueeze(-1) & sel) != 0
+    return m.reshape(*words.shape[:-1], -1)[..., :ncols]
