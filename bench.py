@@ -183,12 +183,16 @@ def bench_entmax(dev, iters=200):
     ms_k = time_region(lambda: fn(*args), iters, 10)
     xl = torch.randn(65536, 1024, generator=g).to(dev)
     ms_l = time_region(lambda: triton_entmax(xl, alpha=1.5, n_iter=10, fast_math=True), 20, 3)
+    yl = torch.empty_like(xl)
+    args_l = (L_.ptr(xl), L_.ptr(yl), 65536, 1024, 1024, 1024, L_.FLA_F32, 1.5, 10, 1, L_.stream_of(xl))
+    ms_lk = time_region(lambda: fn(*args_l), 20, 3)
     return {
         "entmax_cfg1_us": ms * 1e3,
         "entmax_cfg1_GBps": nbytes / (ms * 1e-3) / 1e9,
         "entmax_cfg1_kernel_us": ms_k * 1e3,
         "entmax_cfg1_kernel_GBps": nbytes / (ms_k * 1e-3) / 1e9,
         "entmax_65536x1024_GBps": 2 * 4 * xl.numel() / (ms_l * 1e-3) / 1e9,
+        "entmax_65536x1024_kernel_GBps": 2 * 4 * xl.numel() / (ms_lk * 1e-3) / 1e9,
     }
 
 
@@ -391,7 +395,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline step only (for profiling runs)")
-    ap.add_argument("--only", choices=["cfg2", "cfg4", "lazy", "decode"],
+    ap.add_argument("--only", choices=["cfg2", "cfg4", "lazy", "decode", "entmax"],
                     help="time one of the other configs only and print its figures (for profiling runs)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only copy a 256 MiB buffer 3 times (calibrates the FETCH_SIZE / WRITE_SIZE counters)")
@@ -411,6 +415,9 @@ def main():
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     torch.cuda.synchronize()
+    if args.only == "entmax":
+        print(json.dumps({k_: round(v_, 4) for k_, v_ in bench_entmax(dev).items()}))
+        return
     if args.only:
         print(json.dumps({k_: round(v_, 4) for k_, v_ in bench_configs(dev, args.steps, args.warmup, args.only).items()}))
         return

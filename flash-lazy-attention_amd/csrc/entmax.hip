@@ -12,13 +12,48 @@
 // is the exact root and the iteration stops.  Other alphas stop when a Newton step no
 // longer changes tau in fp32.  The output is renormalised to sum to one, like the
 // entmax package's `ensure_sum_one`.
+#include <type_traits>
+
 #include "common.h"
 #include "flashlazy_internal.h"
 
 namespace fla {
 
 
-template <int DT, int EPL, int MODE>
+// 16 bytes of a row <-> VEC = 16 / sizeof(T) floats.
+template <int DT>
+__device__ __forceinline__ void unpack16(const uint4& w, float* o) {
+  const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+  if constexpr (sizeof(typename Tr<DT>::T) == 4) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = __uint_as_float(u[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      o[2 * i] = Tr<DT>::to_f((typename Tr<DT>::T)(u[i] & 0xffffu));
+      o[2 * i + 1] = Tr<DT>::to_f((typename Tr<DT>::T)(u[i] >> 16));
+    }
+  }
+}
+template <int DT>
+__device__ __forceinline__ uint4 pack16(const float* v) {
+  uint32_t u[4];
+  if constexpr (sizeof(typename Tr<DT>::T) == 4) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) u[i] = __float_as_uint(v[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      u[i] = (uint32_t)Tr<DT>::from_f(v[2 * i]) | ((uint32_t)Tr<DT>::from_f(v[2 * i + 1]) << 16);
+  }
+  return make_uint4(u[0], u[1], u[2], u[3]);
+}
+
+// VIO: rows are read and written in 16-byte pieces (lane l holds elements
+// (c*64 + l)*VEC .. +VEC-1 of chunk c); the launcher uses it when n, the row strides and the
+// base pointers are multiples of 16 bytes.  The threshold only needs the row's values, not
+// their order, so the solver is the same.
+template <int DT, int EPL, int MODE, bool VIO = false>
 __global__ __launch_bounds__(256) void entmax_fwd_kernel(const typename Tr<DT>::T* __restrict__ x,
                                                          typename Tr<DT>::T* __restrict__ y, int64_t rows, int n,
                                                          int64_t ldx, int64_t ldy, float alpha, float beta,
@@ -30,13 +65,31 @@ __global__ __launch_bounds__(256) void entmax_fwd_kernel(const typename Tr<DT>::
   const T* xr = x + row * ldx;
   T* yr = y + row * ldy;
   const float am1 = alpha - 1.0f;
+  constexpr int VEC = 16 / sizeof(T), NCH = EPL / VEC;
   float z[EPL];
   float m = -INFINITY;
+  if constexpr (VIO) {
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) {
-    int j = e * 64 + lane;
-    z[e] = j < n ? Tr<DT>::to_f(xr[j]) * am1 : -INFINITY;
-    m = fmaxf(m, z[e]);
+    for (int c = 0; c < NCH; ++c) {
+      const int j0 = (c * 64 + lane) * VEC;
+      if (j0 < n) {
+        unpack16<DT>(*reinterpret_cast<const uint4*>(xr + j0), z + c * VEC);
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) z[c * VEC + v] *= am1;
+      } else {
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) z[c * VEC + v] = -INFINITY;
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) m = fmaxf(m, z[e]);
+  } else {
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      int j = e * 64 + lane;
+      z[e] = j < n ? Tr<DT>::to_f(xr[j]) * am1 : -INFINITY;
+      m = fmaxf(m, z[e]);
+    }
   }
   m = wave_max(m);
   float tau = m - 1.0f;
@@ -82,10 +135,21 @@ __global__ __launch_bounds__(256) void entmax_fwd_kernel(const typename Tr<DT>::
   }
   S = wave_sum(S);
   const float inv = 1.0f / S;
+  if constexpr (VIO) {
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) {
-    int j = e * 64 + lane;
-    if (j < n) yr[j] = Tr<DT>::from_f(z[e] * inv);
+    for (int c = 0; c < NCH; ++c) {
+      const int j0 = (c * 64 + lane) * VEC;
+      float o[VEC];
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) o[v] = z[c * VEC + v] * inv;
+      if (j0 < n) *reinterpret_cast<uint4*>(yr + j0) = pack16<DT>(o);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      int j = e * 64 + lane;
+      if (j < n) yr[j] = Tr<DT>::from_f(z[e] * inv);
+    }
   }
 }
 
@@ -189,16 +253,31 @@ static hipError_t launch_fwd(const void* x, void* y, int64_t rows, int n, int64_
   const float beta = 1.0f / (alpha - 1.0f);
   const T* xp = (const T*)x;
   T* yp = (T*)y;
+  constexpr int VEC = 16 / sizeof(T);
+  const bool vio = n % VEC == 0 && ldx % VEC == 0 && ldy % VEC == 0 && (uintptr_t)x % 16 == 0 &&
+                   (uintptr_t)y % 16 == 0;
+  auto go = [&](auto epl_tag) {
+    constexpr int EPL = decltype(epl_tag)::value;
+    if constexpr (EPL % VEC == 0) {
+      if (vio) {
+        hipLaunchKernelGGL((entmax_fwd_kernel<DT, EPL, MODE, true>), grid, block, 0, s, xp, yp, rows, n, ldx, ldy,
+                           alpha, beta, maxit);
+        return;
+      }
+    }
+    hipLaunchKernelGGL((entmax_fwd_kernel<DT, EPL, MODE, false>), grid, block, 0, s, xp, yp, rows, n, ldx, ldy,
+                       alpha, beta, maxit);
+  };
   if (n <= 64)
-    hipLaunchKernelGGL((entmax_fwd_kernel<DT, 1, MODE>), grid, block, 0, s, xp, yp, rows, n, ldx, ldy, alpha, beta, maxit);
+    go(std::integral_constant<int, 1>{});
   else if (n <= 128)
-    hipLaunchKernelGGL((entmax_fwd_kernel<DT, 2, MODE>), grid, block, 0, s, xp, yp, rows, n, ldx, ldy, alpha, beta, maxit);
+    go(std::integral_constant<int, 2>{});
   else if (n <= 256)
-    hipLaunchKernelGGL((entmax_fwd_kernel<DT, 4, MODE>), grid, block, 0, s, xp, yp, rows, n, ldx, ldy, alpha, beta, maxit);
+    go(std::integral_constant<int, 4>{});
   else if (n <= 512)
-    hipLaunchKernelGGL((entmax_fwd_kernel<DT, 8, MODE>), grid, block, 0, s, xp, yp, rows, n, ldx, ldy, alpha, beta, maxit);
+    go(std::integral_constant<int, 8>{});
   else if (n <= 1024)
-    hipLaunchKernelGGL((entmax_fwd_kernel<DT, 16, MODE>), grid, block, 0, s, xp, yp, rows, n, ldx, ldy, alpha, beta, maxit);
+    go(std::integral_constant<int, 16>{});
   else
     hipLaunchKernelGGL((entmax_fwd_stream_kernel<DT, MODE>), grid, block, 0, s, xp, yp, rows, n, ldx, ldy, alpha, beta, maxit);
   return hipGetLastError();
