@@ -21,11 +21,13 @@ def _forward(x, alpha, n_iter, fast_math):
         raise ValueError("alpha must lie in (1, 2]")
     shape = x.shape
     n = shape[-1]
-    x2 = x.reshape(-1, n).contiguous()
-    y = torch.empty_like(x2)
+    if not x.is_contiguous():
+        x = x.contiguous()
+    # Rows are the leading dims flattened; y has x's shape, so no reshapes are needed.
+    y = torch.empty(shape, dtype=x.dtype, device=x.device)
+    rows = x.numel() // n if n else 0
     rc = lib().fla_entmax_fwd(
-        ptr(x2), ptr(y), x2.shape[0], n, n, n, DTYPE_CODE[x.dtype], alpha, int(n_iter), int(bool(fast_math)),
-        stream_of(x2),
+        ptr(x), ptr(y), rows, n, n, n, DTYPE_CODE[x.dtype], alpha, int(n_iter), int(bool(fast_math)), stream_of(x),
     )
     check(rc, "fla_entmax_fwd")
     return y, alpha, shape
@@ -37,23 +39,23 @@ class EntmaxFunction(torch.autograd.Function):
         y, alpha, shape = _forward(x, alpha, n_iter, fast_math)
         ctx.alpha = alpha
         ctx.save_for_backward(y)
-        return y.reshape(shape)
+        return y
 
     @staticmethod
     def backward(ctx, dy):
         (y,) = ctx.saved_tensors
         n = y.shape[-1]
-        dy2 = dy.reshape(-1, n).to(y.dtype).contiguous()
-        dx = torch.empty_like(y)
+        dy2 = dy.to(y.dtype).contiguous()
+        dx = torch.empty(y.shape, dtype=y.dtype, device=y.device)
+        rows = y.numel() // n if n else 0
         rc = lib().fla_entmax_bwd(
-            ptr(y), ptr(dy2), ptr(dx), y.shape[0], n, n, n, n, DTYPE_CODE[y.dtype], ctx.alpha, stream_of(y)
+            ptr(y), ptr(dy2), ptr(dx), rows, n, n, n, n, DTYPE_CODE[y.dtype], ctx.alpha, stream_of(y)
         )
         check(rc, "fla_entmax_bwd")
-        return dx.reshape(dy.shape), None, None, None
+        return dx, None, None, None
 
 
 def triton_entmax(x, alpha=1.5, n_iter=10, fast_math=True):
     if torch.is_grad_enabled() and x.requires_grad:
         return EntmaxFunction.apply(x, alpha, n_iter, fast_math)
-    y, _alpha, shape = _forward(x, alpha, n_iter, fast_math)  # no autograd node needed
-    return y.reshape(shape)
+    return _forward(x, alpha, n_iter, fast_math)[0]  # no autograd node needed
