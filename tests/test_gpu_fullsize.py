@@ -266,6 +266,24 @@ def test_config3_sparse_support_mask():
     stats.report()
 
 
+@pytest.mark.parametrize("alpha", [1.5, 2.0])
+def test_long_sequence_L32768(alpha):
+    """Beyond the BASELINE sizes: 32768 keys per row (16-word mask rows, 256 row tiles, lists
+    tightened many times per row), causal, on sampled rows, late mask tiles and a support probe."""
+    banner("long sequence L=32768", alpha)
+    B, H, L, D = 1, 2, 32768, 64
+    x = _gen((B, H, L, D), 77, 4)
+    res = _run_ada(*x, alpha=alpha, causal=True)
+    stats = TieStats(f"L32768 a={alpha}")
+    g = np.random.default_rng(8)
+    for h in range(H):
+        rows = np.unique(np.concatenate([[0, 1, 8191, 8192, L - 129, L - 1], g.choice(L, 10, replace=False)]))
+        _check_rows("L32768", x, res, 0, h, rows, alpha, True, L)
+    _check_mask_tiles("L32768", x, res, 0, 1, [100, 255], alpha, True, L, stats)
+    _check_support_probe("L32768", x, 0, 0, alpha, True, None, _probe_rows(L, L, 4), stats)
+    stats.report()
+
+
 # ---------------------------------------------------------------------------------------------
 # config 4: varlen, 8 sequences of seeded lengths in [512, 8192], H 12
 
