@@ -38,6 +38,7 @@ SIGNATURES = {
     "fla_entmax_fwd": ([_P, _P, _I64, _I64, _I64, _I64, _I, _F, _I, _I, _P], _I),
     "fla_entmax_bwd": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _F, _P], _I),
     "fla_adasplash_mask_words": ([_I], _I),
+    "fla_unpack_block_mask": ([_P, _P, _I64, _I, _I, _P], _I),
     "fla_adasplash_fwd": (
         [_T4, _T4, _T4, _T4, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I, _I, _I, _F, _P],
         _I,
@@ -164,15 +165,12 @@ def prep_varlen(varlen, B, device):
     return vl.to(torch.int32).contiguous()
 
 
-_BITSEL = {}
-
-
 def unpack_block_mask(words, ncols):
-    """int32 [..., R, MW] bit rows (bit c%32 of word c/32 = column c) -> bool [..., R, ncols]."""
-    sel = _BITSEL.get(words.device)
-    if sel is None:  # 1 << c for c = 0..31 as int32 (bit 31 is the sign bit), made once per device
-        sel = torch.tensor([1 << c if c < 31 else -(1 << 31) for c in range(32)], dtype=torch.int32,
-                           device=words.device)
-        _BITSEL[words.device] = sel
-    m = (words.unsqueeze(-1) & sel) != 0
-    return m.reshape(*words.shape[:-1], -1)[..., :ncols]
+    """int32 [..., R, MW] bit rows (bit c%32 of word c/32 = column c) -> bool [..., R, ncols],
+    expanded by one kernel (fla_unpack_block_mask) on the current stream."""
+    words = words.contiguous()
+    out = torch.empty((*words.shape[:-1], ncols), device=words.device, dtype=torch.bool)
+    rows = words.numel() // words.shape[-1] if words.numel() else 0
+    rc = lib().fla_unpack_block_mask(ptr(words), ptr(out), rows, words.shape[-1], ncols, stream_of(words))
+    check(rc, "fla_unpack_block_mask")
+    return out

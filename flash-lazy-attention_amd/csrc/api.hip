@@ -86,6 +86,30 @@ extern "C" int fla_adasplash_mask_words(int L) {
   return (tc + 31) / 32;
 }
 
+namespace {
+__global__ void __launch_bounds__(256) unpack_mask_kernel(const uint32_t* __restrict__ words, uint8_t* __restrict__ out,
+                                                          int64_t n, int mw, int ncols) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int64_t r = i / ncols;
+  const int c = (int)(i - r * ncols);
+  out[i] = (uint8_t)((words[r * mw + (c >> 5)] >> (c & 31)) & 1u);
+}
+}  // namespace
+
+extern "C" int fla_unpack_block_mask(const uint32_t* words, uint8_t* out, int64_t rows, int mw, int ncols,
+                                     void* stream) {
+  if (rows < 0 || mw <= 0 || ncols < 0 || ncols > 32 * mw) return FLA_EINVAL;
+  const int64_t n = rows * ncols;
+  if (n == 0) return FLA_OK;
+  if (!words || !out) return FLA_EINVAL;
+  const int64_t nb = (n + 255) / 256;
+  if (nb > 0x7fffffffLL) return FLA_EINVAL;
+  hipLaunchKernelGGL(unpack_mask_kernel, dim3((unsigned)nb), dim3(256), 0, (hipStream_t)stream, words, out, n, mw,
+                     ncols);
+  return (int)hipGetLastError();
+}
+
 extern "C" int fla_adasplash_fwd(const fla_tensor4_t* q, const fla_tensor4_t* k, const fla_tensor4_t* v,
                                  const fla_tensor4_t* out, float* tau, float* wn, uint32_t* block_mask,
                                  const int32_t* varlen, int B, int H, int Hkv, int L, int D, int dtype, float alpha, int niter,

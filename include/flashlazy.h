@@ -62,6 +62,13 @@ int fla_entmax_bwd(const void* y, const void* dy, void* dx, int64_t rows, int64_
  * p_ij > 0 for a key j of tile c (keys 64c..64c+63). */
 int fla_adasplash_mask_words(int L);
 
+/* Expands a bit-packed block mask (rows of mw uint32 words; bit c%32 of word c/32 = column c,
+ * as written by fla_adasplash_fwd / fla_lazy_fwd) into bytes: out[r * ncols + c] = bit c of
+ * row r (0 or 1), ncols <= 32 * mw, in one launch on the caller's stream.  It yields the
+ * boolean BMASK[b, h, m_block, n_block] of `lazy_attention_triton(..., return_mask=True)`
+ * (reference CURSOR_TASKS.md:240-255, 283-286). */
+int fla_unpack_block_mask(const uint32_t* words, uint8_t* out, int64_t rows, int mw, int ncols, void* stream);
+
 /* AdaSplash forward: out = entmax_alpha(q k^T * scale, masked) v.
  * Replaces `adasplash(q, k, v, alpha, niter, is_causal, varlen)` (block-masked,
  * skip_empty_blocks = 1, block_mask written) and `adasplash_no_block_mask(...)`

@@ -236,3 +236,19 @@ def test_tie_at_row_zero_consistent(dtype):
     tol = 1e-4 if dtype == torch.float32 else 2e-2
     for got, r, n in zip([t.grad for t in ts], ref, ["dq", "dk", "dv", "dbias", "dtau"]):
         assert_close(to_np(got), r, tol * max(1.0, np.abs(r).max() / 4), n)
+
+
+@pytest.mark.parametrize("ncols", [1, 31, 32, 37, 64])
+def test_unpack_block_mask_bits(ncols):
+    # Bit c%32 of word c/32 -> column c, checked against numpy's little-endian bit unpacking
+    # (sign bit 31 and a partial last word included).
+    from adasplash._lib import unpack_block_mask
+
+    banner("unpack_block_mask", ncols)
+    mw = (ncols + 31) // 32
+    w = np.random.default_rng(ncols).integers(-(2**31), 2**31, size=(2, 3, 5, mw), dtype=np.int64).astype(np.int32)
+    w[0, 0, 0, -1] = np.int32(-(2**31))  # only bit 31 of the last word
+    want = np.unpackbits(w.view(np.uint8), axis=-1, bitorder="little").reshape(2, 3, 5, 32 * mw)[..., :ncols]
+    got = unpack_block_mask(torch.from_numpy(w).to(DEV), ncols)
+    assert got.dtype == torch.bool and tuple(got.shape) == (2, 3, 5, ncols)
+    assert np.array_equal(got.cpu().numpy(), want.astype(bool))
