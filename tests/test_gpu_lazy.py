@@ -252,3 +252,36 @@ def test_unpack_block_mask_bits(ncols):
     got = unpack_block_mask(torch.from_numpy(w).to(DEV), ncols)
     assert got.dtype == torch.bool and tuple(got.shape) == (2, 3, 5, ncols)
     assert np.array_equal(got.cpu().numpy(), want.astype(bool))
+
+
+@pytest.mark.parametrize("H,G", [(9, 1), (12, 4)])
+def test_launch_larger_than_one_round_matches_per_head(H, G):
+    """Workgroups are ordered in a serpentine over dispatch rounds of one workgroup per compute
+    unit; with more workgroups than compute units and a partial last round (B = 1, H = 9, L =
+    4096: 288 row tiles on 256 units) the ranks must still cover each (head, row tile) once.
+    Every head is independent, so the full launch equals the heads run one at a time
+    (grids below one round), bit for bit: out, dq, dk, dv, dbias and dtau."""
+    banner("lazy large launch vs per head", H, G)
+    B, L, D, W = 1, 4096, 64, 512
+    Hk = H // G
+    q = rand((B, H, L, D), torch.bfloat16, 50)
+    k, v = (rand((B, Hk, L, D), torch.bfloat16, 51 + i) for i in range(2))
+    do = rand((B, H, L, D), torch.bfloat16, 53)
+    bias = rand((H, W), torch.float32, 54) * 0.02
+    tau = torch.linspace(-1.5, -0.2, H)
+    ts = [t.to(DEV).requires_grad_(True) for t in (q, k, v, bias, tau)]
+    out = _op()(*ts, window_size=W)
+    out.backward(do.to(DEV))
+    for hk in range(Hk):
+        hs = slice(hk * G, (hk + 1) * G)
+        part = [t[:, hs] if i == 0 else (t[:, hk:hk + 1] if i < 3 else t[hs])
+                for i, t in enumerate((q, k, v, bias, tau))]
+        ps = [t.to(DEV).requires_grad_(True) for t in part]
+        o1 = _op()(*ps, window_size=W)
+        o1.backward(do[:, hs].to(DEV))
+        assert torch.equal(out[:, hs], o1), ("out", hk)
+        assert torch.equal(ts[0].grad[:, hs], ps[0].grad), ("dq", hk)
+        assert torch.equal(ts[1].grad[:, hk:hk + 1], ps[1].grad), ("dk", hk)
+        assert torch.equal(ts[2].grad[:, hk:hk + 1], ps[2].grad), ("dv", hk)
+        assert torch.equal(ts[3].grad[hs], ps[3].grad), ("dbias", hk)
+        assert torch.equal(ts[4].grad[hs], ps[4].grad), ("dtau", hk)
