@@ -47,7 +47,7 @@ SIGNATURES = {
         [_T4, _T4, _T4, _T4, _T4, _T4, _T4, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I, _F, _P],
         _I,
     ),
-    "fla_lazy_fwd": ([_T4, _T4, _T4, _T4, _P, _I64, _P, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I, _F, _P], _I),
+    "fla_lazy_fwd": ([_T4, _T4, _T4, _T4, _P, _I64, _P, _I, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I, _F, _P], _I),
     "fla_lazy_bwd_workspace_size": ([_I, _I, _I, _I], ctypes.c_size_t),
     "fla_lazy_decode_workspace_size": ([_I, _I, _I, _I, _I, _I], ctypes.c_size_t),
     "fla_lazy_decode_fwd": (

@@ -30,7 +30,6 @@ from ._lib import (
     ptr,
     stream_of,
     t4,
-    unpack_block_mask,
 )
 
 
@@ -57,17 +56,15 @@ def _forward(q, k, v, bias, tau, window_size, varlen, need_w, want_mask=False):
     out = torch.empty((B, H, L, Dk), device=q.device, dtype=q.dtype)
     lse = torch.empty((B, H, L), device=q.device, dtype=torch.float32)
     wd = torch.empty((B, H, L, Dk), device=q.device, dtype=torch.float32) if need_w else None
-    mask = None
-    if want_mask:
-        mw = lib().fla_adasplash_mask_words(L)
-        mask = torch.empty((B, H, (L + 63) // 64, mw), device=q.device, dtype=torch.int32)
+    # the forward writes the boolean block mask directly (one byte per 64x64 block)
+    nrb = (L + 63) // 64
+    bmask = torch.empty((B, H, nrb, nrb), device=q.device, dtype=torch.bool) if want_mask else None
     rc = lib().fla_lazy_fwd(
         t4(qp), t4(kp), t4(vp), t4(out), ptr(b32), b32.shape[1], ptr(t32), W, ptr(lse), ptr(wd),
-        ptr(mask), int(want_mask), ptr(vl),
+        None, ptr(bmask), int(want_mask), ptr(vl),
         B, H, kp.shape[1], L, Dk, DTYPE_CODE[q.dtype], scale, stream_of(q),
     )
     check(rc, "fla_lazy_fwd")
-    bmask = unpack_block_mask(mask, (L + 63) // 64) if want_mask else None
     return out, lse, wd, (qp, kp, vp), b32, t32, W, vl, D, Dk, scale, bmask
 
 

@@ -200,7 +200,8 @@ extern "C" size_t fla_lazy_bwd_workspace_size(int B, int H, int L, int window) {
 
 extern "C" int fla_lazy_fwd(const fla_tensor4_t* q, const fla_tensor4_t* k, const fla_tensor4_t* v,
                             const fla_tensor4_t* out, const float* bias, int64_t bias_ld, const float* tau,
-                            int window, float* lse, float* wdelta, uint32_t* block_mask, int skip_empty_blocks,
+                            int window, float* lse, float* wdelta, uint32_t* block_mask, uint8_t* block_mask_u8,
+                            int skip_empty_blocks,
                             const int32_t* varlen, int B, int H, int Hkv, int L, int D,
                             int dtype, float scale, void* stream) {
   if (!good_common(B, H, L, D, dtype)) return FLA_EINVAL;
@@ -219,6 +220,7 @@ extern "C" int fla_lazy_fwd(const fla_tensor4_t* q, const fla_tensor4_t* k, cons
   a.lse = lse;
   a.wdelta = wdelta;
   a.mask = block_mask;
+  a.mask8 = block_mask_u8;
   a.skip = skip_empty_blocks ? 1 : 0;
   a.MW = fla_adasplash_mask_words(L);
   a.varlen = varlen;

@@ -48,6 +48,7 @@ struct LazyArgs {
   float* dbias;            // [H, window]
   float* dtau;             // [H]
   uint32_t* mask;          // [B, H, ceil(L/64), MW] bits of (64-row, 64-key) blocks with e > 0, optional
+  uint8_t* mask8;          // [B, H, ceil(L/64), ceil(L/64)] the same blocks, one byte each, optional
   int skip;                // skip the P V products of all-zero (wave, tile) pairs
   int MW;
   int B, H, L, W, nQT;

@@ -106,12 +106,15 @@ int fla_adasplash_bwd(const fla_tensor4_t* q, const fla_tensor4_t* k, const fla_
  *          of word c/32 in row r is set iff some e_ij = relu(p_ij + tau/(i+1)) > 0 with i in rows
  *          64r..64r+63 (i < varlen), j in keys 64c..64c+63 (j <= i, j < varlen) -- the planned
  *          block sparsity of CURSOR_TASKS.md:214-312 (BLOCK_M = BLOCK_N = 64).
+ *   block_mask_u8 [B, H, ceil(L/64), ceil(L/64)] uint8 out, optional: the same blocks, one byte
+ *          (0 / 1) each -- the boolean mask of `return_mask=True`, written by the forward itself.
  *   skip_empty_blocks: skip the P V / wdelta products of all-zero tiles (results unchanged).
  *          The backward cannot skip them: dS = p (m dP - delta) is non-zero where e = 0.
  *   varlen [B] int32, optional. */
 int fla_lazy_fwd(const fla_tensor4_t* q, const fla_tensor4_t* k, const fla_tensor4_t* v, const fla_tensor4_t* out,
                  const float* bias, int64_t bias_ld, const float* tau, int window, float* lse, float* wdelta,
-                 uint32_t* block_mask, int skip_empty_blocks, const int32_t* varlen, int B, int H, int Hkv, int L, int D, int dtype, float scale, void* stream);
+                 uint32_t* block_mask, uint8_t* block_mask_u8, int skip_empty_blocks, const int32_t* varlen, int B,
+                 int H, int Hkv, int L, int D, int dtype, float scale, void* stream);
 
 /* Bytes of caller-provided scratch that fla_lazy_bwd needs (per-tile dbias / dtau partials). */
 size_t fla_lazy_bwd_workspace_size(int B, int H, int L, int window);
