@@ -33,7 +33,7 @@ PEAK_HBM_GBPS = 8000.0
 # HBM bytes per launch of ada_fwd_kernel at the headline config, from two rocprofv3 --pmc
 # passes (FETCH_SIZE x2.000, WRITE_SIZE x1.000 after calibration on a plain 256 MiB copy);
 # source: profiles/adasplash_causal_L8192_a15_traffic.txt.
-FWD_TRAFFIC_BYTES = (157870 * 2.0 + 99385 * 1.0) * 1024
+FWD_TRAFFIC_BYTES = (156277 * 2.0 + 99385 * 1.0) * 1024
 
 
 def dense_flops(B, H, L, D, causal=True):
