@@ -285,3 +285,32 @@ def test_launch_larger_than_one_round_matches_per_head(H, G):
         assert torch.equal(ts[2].grad[:, hk:hk + 1], ps[2].grad), ("dv", hk)
         assert torch.equal(ts[3].grad[hs], ps[3].grad), ("dbias", hk)
         assert torch.equal(ts[4].grad[hs], ps[4].grad), ("dtau", hk)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("L,varlen", [(260, None), (300, [300, 130]), (640, [577, 64])])
+def test_mask_bytes_equal_mask_words(dtype, L, varlen):
+    """The forward writes the block mask in two forms, bit words and one byte per block (the
+    boolean mask of return_mask=True), from the same per-workgroup bits: every byte must equal
+    the corresponding bit, for each dtype's kernel, ragged lengths and an odd number of 64-row
+    blocks (the last workgroup's second block lies past the end)."""
+    banner("lazy mask bytes vs words", dtype, L, varlen)
+    from adasplash._lib import DTYPE_CODE, check, lib, ptr, stream_of, t4, unpack_block_mask
+
+    B, H, D, W = 2, 3, 64, 48
+    q, k, v, bias, tau = _case(B, H, L, D, W, dtype, seed=61, tau=-0.4)
+    q, k, v = (t.to(DEV).contiguous() for t in (q, k, v))
+    b32, t32 = bias.to(DEV), tau.to(DEV)
+    vl = None if varlen is None else torch.tensor(varlen, dtype=torch.int32, device=DEV)
+    nrb, mw = (L + 63) // 64, int(lib().fla_adasplash_mask_words(L))
+    out = torch.empty_like(q)
+    lse = torch.empty((B, H, L), device=DEV, dtype=torch.float32)
+    words = torch.empty((B, H, nrb, mw), device=DEV, dtype=torch.int32)
+    u8 = torch.full((B, H, nrb, nrb), 7, device=DEV, dtype=torch.uint8)
+    rc = lib().fla_lazy_fwd(t4(q), t4(k), t4(v), t4(out), ptr(b32), W, ptr(t32), W, ptr(lse), None,
+                            ptr(words), ptr(u8), 1, ptr(vl), B, H, H, L, D, DTYPE_CODE[dtype], D ** -0.5,
+                            stream_of(q))
+    check(rc, "fla_lazy_fwd")
+    ref = unpack_block_mask(words, nrb)
+    assert torch.equal(u8.bool(), ref) and int(u8.max()) <= 1
+    assert bool(ref.any())
