@@ -353,6 +353,27 @@ __device__ __forceinline__ typename Tr<DT>::frag load_perm_frag(const typename T
   }
 }
 
+// The same fragment as load_perm_frag over a transposed tile, read instead from the row-major
+// [rows][ldr] tile with gfx950's transposing LDS read (16-bit types): in each group of 16 lanes,
+// lane a + 4m supplies the address of 4 consecutive columns of one row, and lane 4a + b receives
+// column b of the rows supplied by lanes a, a+4, a+8, a+12.  Here lane a + 4m of group G points
+// at row row0 + 16j + 4g + m (then + 8), columns col0 + 16 (G & 1) + 4a, so lane l receives column
+// col0 + l % 32 of rows row0 + 16j + 4g + (0..3) and row0 + 16j + 8 + 4g + (0..3) (g = l / 32):
+// the k slots of load_perm_frag / row_of.  No transposed copy of the tile is stored.
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+template <int DT>
+__device__ __forceinline__ typename Tr<DT>::frag load_tr_frag(const typename Tr<DT>::T* tile, int ldr, int row0, int col0,
+                                                              int j, int lane) {
+  static_assert(Tr<DT>::KPL == 8, "16-bit types only");
+  const int G = lane >> 4, i = lane & 15, g = lane >> 5;
+  const typename Tr<DT>::T* p = tile + (row0 + 16 * j + 4 * g + (i >> 2)) * ldr + col0 + 16 * (G & 1) + 4 * (i & 3);
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  const s16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p);
+  const s16x4 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p + 8 * ldr));
+  const uint2 xu = __builtin_bit_cast(uint2, x), yu = __builtin_bit_cast(uint2, y);
+  return __builtin_bit_cast(typename Tr<DT>::frag, make_uint4(xu.x, xu.y, yu.x, yu.y));
+}
+
 // B fragment from accumulator values (registers j*KPL .. j*KPL+KPL-1).
 template <int DT>
 __device__ __forceinline__ typename Tr<DT>::frag acc_frag(const f32x16& a, int j) {
