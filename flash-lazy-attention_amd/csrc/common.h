@@ -238,6 +238,26 @@ __device__ __forceinline__ uint32_t tile_bytes(int64_t ld, int nvalid) {
   return nvalid > 0 ? (uint32_t)(((int64_t)(nvalid - 1) * ld + D) * sizeof(T)) : 0u;
 }
 
+// Row-major LDS layout for 16-bit tiles that are read both by rows (16-byte reads, 16 lanes per
+// LDS cycle) and with the transposing read (8 bytes per lane, 32 lanes per cycle).  Row r starts
+// at element r * D + 8 * shift(r): rows are packed and shifted by whole 16-byte slots so that,
+// with 64 four-byte banks (16 slots of 16 bytes), (a) one 16-byte column of 16 consecutive rows
+// (from a multiple of 16) covers all 16 slots and (b) 64 bytes of columns (from a multiple of 64
+// bytes) of 4 consecutive rows (from a multiple of 4) cover all 16 slots.  A constant row stride
+// cannot do both for D = 32, 64, 128: padding to D + 8 gives (a) but puts rows r and r + 2 of (b)
+// on 8 common banks.  shift is linear over row bases that are multiples of 4:
+// off(r0 + x) = off(r0) + off(x) for r0 % 4 == 0, which keeps fragment offsets immediate.
+static constexpr int RAGGED = -1;  // RowTile LDR value selecting this layout
+template <int D>
+struct Ragged {
+  static_assert(D == 32 || D == 64 || D == 128, "head dims 32, 64, 128");
+  __host__ __device__ static constexpr int shift(int r) {
+    return D == 32 ? (r >> 2) : D == 64 ? 5 * (r >> 2) + 4 * ((r >> 1) & 1) : 13 * (r >> 2) + 4 * (r & 3);
+  }
+  __host__ __device__ static constexpr int off(int r) { return r * D + 8 * shift(r); }
+  __host__ __device__ static constexpr int elems(int rows) { return off(rows - 1) + D; }
+};
+
 // Register-staged tiles for software pipelining: init() fixes each thread's byte offsets once,
 // load() issues the global reads of a tile into registers (rows >= nvalid read as zero),
 // store() writes them to LDS later.
@@ -268,7 +288,14 @@ struct RowTile {
     for (int i = 0; i < PER; ++i) {
       const int c = tid + NT * i;
       const int row = c / CPR, col = (c % CPR) * EPV;
-      if (NCH % NT == 0 || c < NCH) *reinterpret_cast<uint4*>(lds + row * LDR + col) = r[i];
+      if constexpr (LDR == RAGGED) {
+        // row = tid / CPR + i * (NT / CPR), the second part a multiple of 4 (linear in off)
+        static_assert((NT / CPR) % 4 == 0 && NT % CPR == 0, "ragged tile store");
+        if (NCH % NT == 0 || c < NCH)
+          *reinterpret_cast<uint4*>(lds + Ragged<D>::off(tid / CPR) + Ragged<D>::off(i * (NT / CPR)) + col) = r[i];
+      } else {
+        if (NCH % NT == 0 || c < NCH) *reinterpret_cast<uint4*>(lds + row * LDR + col) = r[i];
+      }
     }
   }
 };
@@ -370,6 +397,28 @@ __device__ __forceinline__ typename Tr<DT>::frag load_tr_frag(const typename Tr<
   typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
   const s16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p);
   const s16x4 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p + 8 * ldr));
+  const uint2 xu = __builtin_bit_cast(uint2, x), yu = __builtin_bit_cast(uint2, y);
+  return __builtin_bit_cast(typename Tr<DT>::frag, make_uint4(xu.x, xu.y, yu.x, yu.y));
+}
+
+// Element offset of row r in a row-major tile of row stride LDR, or of the ragged layout.
+template <int LDR, int D>
+__device__ __forceinline__ constexpr int row_off(int r) {
+  if constexpr (LDR == RAGGED) return Ragged<D>::off(r);
+  else return r * LDR;
+}
+
+// load_tr_frag over a tile of layout LDR (a stride or RAGGED); row0 a multiple of 16.
+template <int DT, int LDR, int D>
+__device__ __forceinline__ typename Tr<DT>::frag load_tr_frag_l(const typename Tr<DT>::T* tile, int row0, int col0, int j,
+                                                                int lane) {
+  static_assert(Tr<DT>::KPL == 8, "16-bit types only");
+  const int G = lane >> 4, i = lane & 15, g = lane >> 5;
+  const typename Tr<DT>::T* p =
+      tile + row_off<LDR, D>(row0 + 16 * j) + row_off<LDR, D>(4 * g + (i >> 2)) + col0 + 16 * (G & 1) + 4 * (i & 3);
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  const s16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p);
+  const s16x4 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p + row_off<LDR, D>(8)));
   const uint2 xu = __builtin_bit_cast(uint2, x), yu = __builtin_bit_cast(uint2, y);
   return __builtin_bit_cast(typename Tr<DT>::frag, make_uint4(xu.x, xu.y, yu.x, yu.y));
 }
