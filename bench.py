@@ -49,9 +49,13 @@ def time_region(fn, steps, warmup, min_warm_s=0.2):
     """Mean ms per call of fn over `steps` calls, timed with events on the current stream.
     The warm-up runs at least `warmup` calls and at least `min_warm_s` seconds: after the GPU
     has idled (host work between regions), its clock takes ~20-30 ms of work to return to
-    steady state, and calls in that window run up to ~25% slow."""
+    steady state, and calls in that window run up to ~25% slow.  The time window starts after
+    the first call has finished, whose one-time set-up (module loads, first allocations) can
+    alone outlast it."""
+    fn()
+    torch.cuda.synchronize()
     t_end = time.perf_counter() + min_warm_s
-    n = 0
+    n = 1
     while n < warmup or time.perf_counter() < t_end:
         fn()
         n += 1
