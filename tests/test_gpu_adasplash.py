@@ -33,7 +33,7 @@ def _inputs(B, H, L, D, dtype, seed=42, scale=1.0):
 
 @pytest.mark.parametrize("B,H", [(1, 1), (2, 2)])
 @pytest.mark.parametrize("L", [128, 256])
-@pytest.mark.parametrize("D", [32, 64])
+@pytest.mark.parametrize("D", [32, 64, 128])
 @pytest.mark.parametrize("alpha", [1.333, 1.5, 2.0])
 @pytest.mark.parametrize("is_causal", [False, True])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32, torch.bfloat16])
@@ -118,9 +118,12 @@ def test_backward_fp32(L, alpha, masked):
 @pytest.mark.parametrize("alpha", [1.5, 2.0, 1.333])
 @pytest.mark.parametrize("is_causal", [False, True])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_backward_lowp_varlen(alpha, is_causal, dtype):
-    banner("ada bwd lowp", alpha, is_causal, dtype)
-    B, H, L, D = 2, 2, 320, 64
+@pytest.mark.parametrize("D", [32, 64, 128])
+def test_backward_lowp_varlen(alpha, is_causal, dtype, D):
+    # 16-bit tiles use a head-dim-specific LDS layout (rows shifted per head dim), so every
+    # supported D is compared with the oracle
+    banner("ada bwd lowp", alpha, is_causal, dtype, D)
+    B, H, L = 2, 2, 320
     q, k, v = _inputs(B, H, L, D, dtype, seed=11)
     do = rand((B, H, L, D), dtype, 12)
     varlen = np.array([320, 199])
@@ -128,8 +131,13 @@ def test_backward_lowp_varlen(alpha, is_causal, dtype):
     qd, kd, vd = (t.to(DEV).requires_grad_(True) for t in (q, k, v))
     out = _ops()[0](qd, kd, vd, alpha=alpha, is_causal=is_causal, varlen=torch.tensor(varlen, device=DEV))
     out.backward(do.to(DEV))
+    # P and dS enter the gradient products rounded to 16 bits (bf16: 2^-8 relative).  A row of
+    # dQ = sum_j dS_ij k_j can cancel, so its absolute error follows sum_j |dS_ij k_j| rather than
+    # |dQ_i|: typically up to ~0.4% of max|ref| at D = 32, 64, 128 alike, 1% on a cancelling row
+    # (D = 32, alpha = 1.333).  The bound is 2% of max|ref| (at least 2e-2); a wrong operand or
+    # layout gives errors of the order of max|ref| itself.
     for got, r, n in zip((qd.grad, kd.grad, vd.grad), ref, "qkv"):
-        assert_close(to_np(got), r, 2e-2 * max(1.0, np.abs(r).max() / 4), f"d{n}")
+        assert_close(to_np(got), r, 2e-2 * max(1.0, np.abs(r).max()), f"d{n}")
     for b in range(B):
         n = varlen[b]
         for gt in (qd.grad, kd.grad, vd.grad):
